@@ -1,0 +1,212 @@
+/* mimizuku_amd — C ABI of the MI355X (gfx950) Whisper compute path.
+ *
+ * This is the drop-in boundary that replaces the reference's cudarc-based device layer (src/gpu.rs), its CUDA
+ * kernels (kernels/whisper.cu) and its engine (src/model.rs, src/transcribe.rs). Plain C: opaque handles, device
+ * pointers as uint64_t (as the reference's `Ptr = u64`, src/gpu.rs:12), sizes in bytes or elements as stated.
+ * Every function returns 0 on success or a nonzero MZ_ERR_* code; mz_last_error() then holds a message for the
+ * calling thread (the reference returns R<T> = Result<T, Box<dyn Error>>, src/gpu.rs:11).
+ *
+ * Work is enqueued on the context's one non-default stream (src/gpu.rs:125); functions that return host data
+ * synchronise it. One host thread drives one context.
+ */
+#ifndef MIMIZUKU_H
+#define MIMIZUKU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MZ_OK 0
+#define MZ_ERR_HIP 1   /* HIP runtime error or no device */
+#define MZ_ERR_ARG 2   /* invalid argument, shape or size */
+#define MZ_ERR_STATE 3 /* call out of order (e.g. step before weights are loaded) */
+
+typedef struct mz_ctx mz_ctx;
+typedef struct mz_graph mz_graph;
+typedef struct mz_engine mz_engine;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* mz_last_error(void);
+const char* mz_version(void);
+
+/* ------------------------------------------------------------------ runtime (src/gpu.rs `Gpu`) */
+
+/* Device `device`, one non-blocking stream. Replaces Gpu::new (src/gpu.rs:122-137); no library handles. */
+int mz_init(int device, mz_ctx** out);
+int mz_ctx_free(mz_ctx* c);
+/* Zero-filled device buffer of max(bytes, 16) bytes (Gpu::alloc, src/gpu.rs:140-145). Freed by mz_free or at
+ * mz_ctx_free. */
+int mz_alloc(mz_ctx* c, size_t bytes, uint64_t* dptr);
+int mz_free(mz_ctx* c, uint64_t dptr);
+/* (free, total) device bytes (Gpu::mem_info, src/gpu.rs:152-154). */
+int mz_mem_info(mz_ctx* c, size_t* free_bytes, size_t* total_bytes);
+/* Host -> device, then synchronise (Gpu::upload, src/gpu.rs:160-163). */
+int mz_upload(mz_ctx* c, uint64_t dst, const void* src, size_t bytes);
+/* Device -> host after the stream's work (Gpu::download, src/gpu.rs:171-176). */
+int mz_download(mz_ctx* c, void* dst, uint64_t src, size_t bytes);
+/* Device -> device, asynchronous and capturable (Gpu::copy, src/gpu.rs:249-252). */
+int mz_copy(mz_ctx* c, uint64_t dst, uint64_t src, size_t bytes);
+int mz_sync(mz_ctx* c); /* Gpu::sync, src/gpu.rs:182-185 */
+/* Timing events on the context's stream. */
+int mz_event_create(mz_ctx* c, uint64_t* ev);
+int mz_event_record(mz_ctx* c, uint64_t ev);
+int mz_event_elapsed_ms(uint64_t start, uint64_t stop, float* ms);
+int mz_event_destroy(uint64_t ev);
+
+/* Stream capture into a replayable graph (cudarc begin_capture / end_capture / Graph::{upload, launch},
+ * src/transcribe.rs:123-135): thread-local capture mode, graph uploaded once, one launch per replay. */
+int mz_graph_begin(mz_ctx* c);
+int mz_graph_end(mz_ctx* c, mz_graph** out);
+int mz_graph_launch(mz_ctx* c, mz_graph* g);
+int mz_graph_free(mz_graph* g);
+
+/* ------------------------------------------------------------------ kernels (device pointers, the ctx stream) */
+
+/* y[m][n] (row stride ldy, fp16) = x[m][k] (row stride ldx) . W[n][k]^T + bias[n] (bias may be 0), fp32
+ * accumulation, one rounding — the semantics of Gpu::gemm (src/gpu.rs:208-236). k % 64 == 0, n % 4 == 0.
+ * m <= 32 per tile uses the decode-sized kernel (the reference's gemv_* for m <= 8), larger m the tiled MFMA GEMM
+ * (cuBLAS there). */
+int mz_gemm(mz_ctx* c, uint64_t x, int ldx, uint64_t w, uint64_t y, int ldy, int m, int n, int k, uint64_t bias);
+
+#define MZ_EPI_F16 0       /* out f16 [m][ldo] = acc + bias */
+#define MZ_EPI_GELU_F16 1  /* out f16 [m][ldo] = gelu(acc + bias) (fc1; gelu_inplace fused, whisper.cu:106-113) */
+#define MZ_EPI_RESID_F32 2 /* out f32 [m][ldo] += acc + bias (residual add fused into out-proj / fc2) */
+#define MZ_EPI_GELU_POS 3  /* out f32 [m][ldo] = gelu(acc + bias) + pos[m % 1500][n] (conv2 + add_pos, whisper.cu:115-119) */
+#define MZ_EPI_HEADS 4     /* scatter into 1536 x 64 per-head tiles; v tiles transposed (see mz_linear_args) */
+
+/* One encoder-sized product on the tiled MFMA kernel (replaces fill_bias + cublasGemmStridedBatchedEx,
+ * src/gpu.rs:229-235, and im2col1/im2col2, whisper.cu:121-139, when conv_cin > 0). */
+typedef struct {
+    int epilogue;
+    uint64_t a;   /* f16 [m][lda]; with conv_cin > 0 the conv source rows [clips * conv_tin][conv_cin] */
+    long lda;
+    uint64_t w;   /* f16 [n][k]; for a conv, columns ordered tap-major: w'[co][tap * cin + ci] */
+    uint64_t bias;
+    int m, n, k;
+    uint64_t out;
+    long ldo;
+    uint64_t pos; /* MZ_EPI_GELU_POS: f16 [1500][n] */
+    /* MZ_EPI_HEADS: column n -> block n / 64, row m -> clip m / 1500, time m % 1500; the block's tile is at
+     * heads + ((slot0 + clip) * blocks_per_clip + block) * 1536 * 64 halves. kind 3: blocks [q|k|v][head] (encoder
+     * self-attention), kind 2: [layer][k|v][head] (cross-attention); v tiles are stored transposed [64][1536]. */
+    uint64_t heads;
+    int blocks_per_clip, nh, kind, slot0;
+    /* implicit conv1d (kernel 3, padding 1): A[clip * conv_tout + t][tap * cin + ci] =
+     * src[(clip * conv_tin + conv_stride * t + tap - 1) * cin + ci], zero outside; k >= 3 * cin padded with 0 */
+    int conv_cin, conv_tin, conv_tout, conv_stride;
+} mz_linear_args;
+int mz_linear(mz_ctx* c, const mz_linear_args* a);
+
+/* y[r] = LayerNorm(x[r]) for fp32 rows x (row stride ldx) into fp16 y (layernorm, whisper.cu:65-69). */
+int mz_layernorm(mz_ctx* c, uint64_t x, long ldx, uint64_t w, uint64_t b, uint64_t y, long ldy, int rows, int dim,
+                 float eps);
+/* x[r] += d[r] (fp32 x, fp16 d) in place, then y[r] = LayerNorm(x[r]) (add_layernorm, whisper.cu:71-82). */
+int mz_add_layernorm(mz_ctx* c, uint64_t x, uint64_t d, uint64_t w, uint64_t b, uint64_t y, int rows, int dim,
+                     float eps);
+/* Encoder self-attention (enc_flash, whisper.cu:168-299): qkvh [clips][3][nh] tiles of 1536 x 64 halves
+ * (q, k as [t][64]; v transposed [64][t]; t >= 1500 zero) -> out f16 [clips * 1500][nh * 64]; scale 1/8. */
+int mz_enc_attention(mz_ctx* c, uint64_t qkvh, uint64_t out, int clips, int nh);
+/* log-mel f32 [clips][n_mels][3000] -> f16 [clips][3000][n_mels] (the conv stem's source layout). */
+int mz_mel_transpose(mz_ctx* c, uint64_t mel, uint64_t melT, int clips, int n_mels);
+
+/* ------------------------------------------------------------------ engine (src/model.rs, src/transcribe.rs) */
+
+/* Model geometry (Dims, src/model.rs:14-25). */
+typedef struct {
+    int d, ff, nh, enc_layers, dec_layers, n_mels, vocab, max_t;
+} mz_dims;
+
+/* Generation settings (GenCfg, src/model.rs:64-76), as plain arrays. */
+typedef struct {
+    int sot, eos, no_timestamps;
+    const int32_t* suppress;
+    int n_suppress;
+    const int32_t* begin_suppress; /* at most 2 */
+    int n_begin_suppress;
+    const int32_t* lang_tokens; /* language tokens (detection restricts the choice to these) */
+    int n_langs;
+    const int32_t* align_heads; /* (layer, head) pairs */
+    int n_align;
+} mz_gencfg;
+
+/* Device bytes the engine allocates besides the weights (scratch_bytes, src/model.rs:324-330). */
+size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int eg);
+/* Validates the geometry (Dims::load checks, src/model.rs:47-59) and allocates the engine for bmax decoded rows and
+ * eg clips per encoder pass (Engine::new, src/model.rs:333-514, minus reading files). */
+int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, int bmax, int eg, mz_engine** out);
+#define MZ_DT_F16 0
+#define MZ_DT_F32 1
+/* Places one checkpoint tensor by its Hugging Face name (Loader, src/model.rs:200-265): shape-checked, F32
+ * converted to F16, q/k/v fused (zero k bias), every decoder layer's cross k/v fused, conv weights reordered
+ * tap-major. Unknown names are ignored. */
+int mz_engine_put(mz_engine* e, const char* name, int dtype, const void* data, const int64_t* shape, int ndim);
+/* Checks every tensor was placed (Arena::finish, src/gpu.rs:363-373). */
+int mz_engine_finish(mz_engine* e);
+/* Encoder for n <= eg clips of log-mel f32 [n][n_mels][3000] (host); writes every decoder layer's cross k/v into
+ * decoder slots slot0 .. slot0 + n - 1 (Engine::encode, src/model.rs:545-625). */
+int mz_engine_encode(mz_engine* e, const float* mels, int n, int slot0);
+/* Prompt tokens [n][prompt_len] into rows 0..n-1, every row unfinished, position 0 (Engine::reset, :628-637). */
+int mz_engine_reset(mz_engine* e, const int32_t* prompts, int n, int prompt_len);
+/* One step on the start token restricted to language tokens; writes token 1 of each row and returns them in
+ * langs[b] (Engine::detect, :641-646). */
+int mz_engine_detect(mz_engine* e, int b, int32_t* langs);
+/* One greedy step for rows 0..b-1: feed token p, choose token p + 1 (positions below prompt_len stay), p += 1
+ * (Engine::step, :650-736). lang != 0 restricts the choice to language tokens. */
+int mz_engine_step(mz_engine* e, int b, int lang, int prompt_len);
+/* Capture step(b, 0, prompt_len) once as a graph and upload it; replay launches it (transcribe.rs:123-142). */
+int mz_engine_capture(mz_engine* e, int b, int prompt_len);
+int mz_engine_replay(mz_engine* e);
+/* Keep a copy of every encoder layer's input (fp32 residual stream) of the next encode (Engine::trace). */
+int mz_engine_set_trace(mz_engine* e, int on);
+
+#define MZ_BUF_TOK 0     /* i32 [bmax][max_t] */
+#define MZ_BUF_DONE 1    /* i32 [bmax] */
+#define MZ_BUF_CTR 2     /* i32 [4]; ctr[0] = position of the next step */
+#define MZ_BUF_ALIGN 3   /* f16 [bmax][max_t][n_align][1500] alignment-head probabilities */
+#define MZ_BUF_ENC_OUT 4 /* f16 [eg * 1500][d] final-LN encoder output of the last encode */
+#define MZ_BUF_LOGITS 5  /* f32 [bmax][vocab] logits of the last step */
+#define MZ_BUF_TRACE 6   /* f32 [enc_layers][eg * 1500][d] encoder layer inputs (set_trace) */
+#define MZ_BUF_XKV 7     /* f16 [bmax][dec_layers][2][nh] tiles of 1536 x 64 (k as [t][64], v transposed) */
+#define MZ_BUF_DEC_X 8   /* f32 [bmax][d] decoder residual stream */
+#define MZ_BUF_ENC_X 9   /* f32 [eg * 1500][d] encoder residual stream */
+/* Device address and size of an engine buffer. */
+int mz_engine_buffer(mz_engine* e, int which, uint64_t* dptr, size_t* bytes);
+/* Synchronise, then copy bytes at byte offset `offset` of an engine buffer to host memory. */
+int mz_engine_read(mz_engine* e, int which, void* dst, size_t offset, size_t bytes);
+int mz_engine_free(mz_engine* e);
+
+/* Wall times of the stages, seconds (Times, src/transcribe.rs:95-101). */
+typedef struct {
+    double enc, dec, post;
+    int steps;
+} mz_times;
+
+/* Encode and greedily decode n <= bmax clips of log-mel f32 [n][n_mels][3000] with token timestamps
+ * (transcribe, src/transcribe.rs:104-167). frames[i] = 10 ms frames of audio in clip i (3000 for a full window).
+ * prompt = [sot, lang, task, notimestamps] (lang ignored when detect != 0). max_new caps the generated tokens
+ * (<= 0: up to max_t - prompt_len, as the reference). half_align != 0 rounds the timestamp arithmetic through fp16
+ * as the reference does (src/align.rs). Outputs per clip i: seq[i * max_t ..] tokens, seq_len[i], ts[i * max_t ..]
+ * start times, langs[i]. */
+int mz_transcribe(mz_engine* e, const float* mels, const int32_t* frames, int n, const int32_t* prompt,
+                  int prompt_len, int detect, int use_graph, int max_new, int half_align, int32_t* seq,
+                  int32_t* seq_len, float* ts, int32_t* langs, mz_times* times);
+
+/* ------------------------------------------------------------------ host helpers */
+
+/* Token start times from alignment-head weights w [rows][heads][cols_full] (f32), cropped to cols frames
+ * (jump_times, src/align.rs:8-63); out[rows]. */
+int mz_jump_times(const float* w, int rows, int heads, int cols_full, int cols, int width, int half, float* out);
+/* Dynamic time warping on cost m [rows][cols] (dtw, src/align.rs:66-106); path written to text/time (capacity
+ * rows + cols), its length to *len. */
+int mz_dtw(const double* m, int rows, int cols, int32_t* text, int32_t* time, int32_t* len);
+/* IEEE binary16 conversions, round to nearest even (h2f / f2h, src/gpu.rs:79-114). */
+uint16_t mz_f2h(float x);
+float mz_h2f(uint16_t h);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MIMIZUKU_H */

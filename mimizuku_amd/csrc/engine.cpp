@@ -1,0 +1,796 @@
+// The Whisper engine behind the C ABI: weight placement, the encoder pass, the decoder step (captured as one graph
+// with the position in device memory) and the batch transcription loop. Mirrors src/model.rs (Engine::{new, encode,
+// reset, detect, step}) and src/transcribe.rs (transcribe), with its own kernels and data layouts:
+//   * the residual streams are fp32 (encoder [clips*1500][d], decoder [bmax][d]); GEMM operands are fp16;
+//   * encoder q/k/v and every decoder layer's cross k/v are stored per head as 1536 x 64 tiles, v transposed;
+//   * the self-attention cache is per (row, head): k [max_t][64], v transposed [64][max_t].
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+#include <map>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "../../include/mimizuku.h"
+#include "mz_internal.h"
+#include "mz_kernels.h"
+
+namespace {
+
+constexpr int HD = 64, TENC = 1500, TPAD = 1536, NFR = 3000;
+constexpr float EPS = 1e-5f;
+constexpr int XCHUNK = 384;  // cross-attention keys per block (4 blocks per row and head)
+
+struct Ln {
+    f16 *w = nullptr, *b = nullptr;
+};
+struct Lin {
+    f16 *w = nullptr, *b = nullptr;
+};
+struct EncLayer {
+    Ln ln1, ln2;
+    Lin qkv, o, fc1, fc2;
+};
+struct DecLayer {
+    Ln ln1, lnx, ln3;
+    Lin qkv, o, xq, xo, fc1, fc2;
+};
+
+// where a checkpoint tensor goes: rows [row0, row0 + rows) of a [.][cols] destination
+struct Slot {
+    f16* dst;
+    std::vector<int64_t> shape;
+    int kind;  // 0 plain copy, 1 conv weight reordered tap-major into rows of kpad columns
+    int kpad;
+};
+
+inline int rup(int x, int m) { return (x + m - 1) / m * m; }
+
+}  // namespace
+
+struct mz_engine {
+    mz_ctx* c = nullptr;
+    mz_dims dm{};
+    int bmax = 0, eg = 0, na = 0;
+    int sot = 0, eos = 0, bs1 = -1, bs2 = -1;
+    std::vector<int> align_heads;  // pairs
+    bool trace_on = false;
+    bool loaded = false;
+
+    // weights
+    f16* arena = nullptr;
+    size_t arena_elems = 0, arena_used = 0;
+    std::map<std::string, Slot> slots;
+    std::set<std::string> placed;
+    EncLayer* enc = nullptr;
+    DecLayer* dec = nullptr;
+    std::vector<EncLayer> encv;
+    std::vector<DecLayer> decv;
+    Lin conv1, conv2, xkv;
+    Ln eln, dln;
+    f16 *epos = nullptr, *emb = nullptr, *dpos = nullptr;
+    int k1pad = 0;
+
+    // encoder scratch (eg clips)
+    float* mel = nullptr;
+    f16 *melT = nullptr, *h1 = nullptr, *hb = nullptr, *qkvh = nullptr, *att = nullptr, *ff = nullptr;
+    float *ex = nullptr, *trace = nullptr;
+    // decoder state (bmax rows)
+    f16* xkvbuf = nullptr;
+    int *tok = nullptr, *done = nullptr, *ctr = nullptr;
+    float *x = nullptr, *q = nullptr, *part = nullptr, *logits = nullptr;
+    f16 *h = nullptr, *datt = nullptr, *dff = nullptr, *kc = nullptr, *vct = nullptr, *align = nullptr;
+    float *xpart = nullptr, *sal = nullptr;
+    unsigned *xcnt = nullptr, *acnt = nullptr;
+    int* aslot = nullptr;
+    unsigned char *sup = nullptr, *sup_lang = nullptr;
+    size_t part_elems = 0;
+    mz_graph* graph = nullptr;
+    int graph_b = -1, graph_np = -1;
+
+    template <class T>
+    int alloc(T** p, size_t n) {
+        void* v;
+        if (int r = mz_ctx_alloc(c, n * sizeof(T), &v)) return r;
+        *p = (T*)v;
+        return MZ_OK;
+    }
+    f16* take(size_t n) {
+        f16* p = arena + arena_used;
+        arena_used += (n + 127) / 128 * 128;  // 256-byte aligned tensors
+        return p;
+    }
+};
+
+namespace {
+
+size_t weight_elems(const mz_dims& d, int* k1pad) {
+    const size_t D = d.d, F = d.ff;
+    auto r = [](size_t n) { return (n + 127) / 128 * 128; };
+    *k1pad = rup(3 * d.n_mels, 64);
+    size_t n = r(D * *k1pad) + r(D) + r(D * 3 * D) + r(D) + r((size_t)TENC * D) + 2 * r(D);
+    size_t enc = 4 * r(D) + r(3 * D * D) + r(3 * D) + r(D * D) + r(D) + r(F * D) + r(F) + r(D * F) + r(D);
+    size_t dec = 6 * r(D) + r(3 * D * D) + r(3 * D) + 3 * (r(D * D) + r(D)) + r(F * D) + r(F) + r(D * F) + r(D);
+    n += d.enc_layers * enc + d.dec_layers * dec;
+    n += r((size_t)d.dec_layers * 2 * D * D) + r((size_t)d.dec_layers * 2 * D);
+    n += r((size_t)d.vocab * D) + r((size_t)d.max_t * D) + 2 * r(D);
+    return n;
+}
+
+int ksplit_for(int N, int K) {
+    // split K until the grid has a few hundred blocks, keeping >= 4 groups of 64 per block (one per wave)
+    const int tiles = (N + 31) / 32, groups = K / 64;
+    int best = 1;
+    for (int ks = 1; ks <= groups; ks++) {
+        if (groups % ks || groups / ks < 4) continue;
+        if ((long)tiles * ks > 1024) break;
+        best = ks;
+        if ((long)tiles * ks >= 256) break;
+    }
+    return best;
+}
+
+}  // namespace
+
+extern "C" size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int eg) {
+    if (!d) return 0;
+    const size_t D = d->d, F = d->ff, nl = d->dec_layers, nh = d->nh, mt = d->max_t, V = d->vocab;
+    const size_t B = bmax, G = eg;
+    size_t enc = G * d->n_mels * NFR * 4 + G * NFR * d->n_mels * 2 + G * NFR * D * 2 + G * TENC * D * 4 +
+                 G * TENC * D * 2 * 2 + G * 3 * nh * TPAD * HD * 2 + G * TENC * F * 2;
+    size_t dec = B * nl * 2 * nh * TPAD * HD * 2 + B * mt * 4 + B * 4 + 16 + B * D * 4 * 2 + B * D * 2 * 2 + B * F * 2 +
+                 2 * nl * B * nh * mt * HD * 2 + B * V * 4 + B * mt * n_align * TENC * 2 + B * nh * 4 * 66 * 4 +
+                 B * nh * 4 + B * n_align * TPAD * 4 + nl * nh * 4 + 2 * V;
+    size_t part = 20 * B * D * 4 + 4 * B * F * 4;
+    return enc + dec + part;
+}
+
+extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, int bmax, int eg, mz_engine** out) {
+    if (!c || !d || !g || !out) return mz_fail(MZ_ERR_ARG, "mz_engine_new: null argument");
+    *out = nullptr;
+    // geometry limits (Dims::load, src/model.rs:47-59) plus this build's: rows of dim % 128 == 0 and <= 2048
+    if (d->nh * HD != d->d || d->d % 128 || d->d > 2048 || d->ff % 64 || d->ff <= 0 || d->n_mels % 8 ||
+        d->n_mels <= 0 || d->max_t < 16 || d->max_t > 448 || d->max_t % 8 || d->enc_layers < 1 || d->enc_layers > 64 ||
+        d->dec_layers < 1 || d->dec_layers > 64 || d->vocab <= 0)
+        return mz_fail(MZ_ERR_ARG,
+                       "unsupported shape d=%d ff=%d nh=%d n_mels=%d max_t=%d layers=%d/%d: the kernels need 64-wide "
+                       "heads, d %% 128 == 0 (<= 2048), ff %% 64 == 0, n_mels %% 8 == 0, max_t %% 8 == 0 in [16, 448]",
+                       d->d, d->ff, d->nh, d->n_mels, d->max_t, d->enc_layers, d->dec_layers);
+    if (bmax <= 0 || eg <= 0 || eg > bmax) return mz_fail(MZ_ERR_ARG, "bmax %d / enc group %d", bmax, eg);
+    if (g->n_begin_suppress > 2) return mz_fail(MZ_ERR_ARG, "more than two begin_suppress tokens are not supported");
+    if (g->n_align <= 0) return mz_fail(MZ_ERR_ARG, "alignment_heads is empty");
+    std::set<std::pair<int, int>> uniq;
+    for (int i = 0; i < g->n_align; i++) {
+        int l = g->align_heads[2 * i], hh = g->align_heads[2 * i + 1];
+        if (l < 0 || l >= d->dec_layers || hh < 0 || hh >= d->nh)
+            return mz_fail(MZ_ERR_ARG, "alignment head (%d, %d) outside the model", l, hh);
+        uniq.insert({l, hh});
+    }
+    if ((int)uniq.size() != g->n_align) return mz_fail(MZ_ERR_ARG, "alignment_heads has duplicates");
+    for (int t : {g->sot, g->eos, g->no_timestamps})
+        if (t < 0 || t >= d->vocab) return mz_fail(MZ_ERR_ARG, "special token %d out of range", t);
+
+    auto* e = new mz_engine();
+    e->c = c;
+    e->dm = *d;
+    e->bmax = bmax;
+    e->eg = eg;
+    e->na = g->n_align;
+    e->sot = g->sot;
+    e->eos = g->eos;
+    e->bs1 = g->n_begin_suppress > 0 ? g->begin_suppress[0] : -1;
+    e->bs2 = g->n_begin_suppress > 1 ? g->begin_suppress[1] : -1;
+    e->align_heads.assign(g->align_heads, g->align_heads + 2 * g->n_align);
+    auto fail = [&](int r) {
+        mz_engine_free(e);
+        return r;
+    };
+
+    // pre-flight memory check (src/model.rs:343-357)
+    const size_t welems = weight_elems(*d, &e->k1pad);
+    const size_t need = welems * 2 + mz_scratch_bytes(d, e->na, bmax, eg);
+    size_t fr = 0, tot = 0;
+    if (hipMemGetInfo(&fr, &tot) == hipSuccess && need > tot)
+        return fail(mz_fail(MZ_ERR_ARG, "not enough GPU memory: about %.1f GB needed for bmax %d / enc group %d, %.1f GB total",
+                            need / 1e9, bmax, eg, tot / 1e9));
+
+    if (int r = e->alloc(&e->arena, welems)) return fail(r);
+    e->arena_elems = welems;
+    const int D = d->d, F = d->ff, nl = d->dec_layers, nh = d->nh, mt = d->max_t, V = d->vocab;
+    const int64_t D6 = D;
+    auto lin = [&](Lin& L, const std::string& p, int n, int k, bool bias_from_ckpt = true) {
+        L.w = e->take((size_t)n * k);
+        L.b = e->take(n);
+        e->slots[p + ".weight"] = Slot{L.w, {n, k}, 0, 0};
+        if (bias_from_ckpt) e->slots[p + ".bias"] = Slot{L.b, {n}, 0, 0};
+    };
+    auto ln = [&](Ln& L, const std::string& p) {
+        L.w = e->take(D);
+        L.b = e->take(D);
+        e->slots[p + ".weight"] = Slot{L.w, {D6}, 0, 0};
+        e->slots[p + ".bias"] = Slot{L.b, {D6}, 0, 0};
+    };
+    auto qkv = [&](Lin& L, const std::string& p) {  // q, k, v fused into [3D][D]; k has no bias (zeros)
+        L.w = e->take((size_t)3 * D * D);
+        L.b = e->take(3 * D);
+        e->slots[p + ".q_proj.weight"] = Slot{L.w, {D6, D6}, 0, 0};
+        e->slots[p + ".k_proj.weight"] = Slot{L.w + (size_t)D * D, {D6, D6}, 0, 0};
+        e->slots[p + ".v_proj.weight"] = Slot{L.w + (size_t)2 * D * D, {D6, D6}, 0, 0};
+        e->slots[p + ".q_proj.bias"] = Slot{L.b, {D6}, 0, 0};
+        e->slots[p + ".v_proj.bias"] = Slot{L.b + 2 * D, {D6}, 0, 0};
+    };
+    // conv weights [D][cin][3] -> tap-major rows w'[co][tap * cin + ci], K padded to a multiple of 64
+    e->conv1.w = e->take((size_t)D * e->k1pad);
+    e->conv1.b = e->take(D);
+    e->slots["model.encoder.conv1.weight"] = Slot{e->conv1.w, {D6, d->n_mels, 3}, 1, e->k1pad};
+    e->slots["model.encoder.conv1.bias"] = Slot{e->conv1.b, {D6}, 0, 0};
+    e->conv2.w = e->take((size_t)D * 3 * D);
+    e->conv2.b = e->take(D);
+    e->slots["model.encoder.conv2.weight"] = Slot{e->conv2.w, {D6, D6, 3}, 1, 3 * D};
+    e->slots["model.encoder.conv2.bias"] = Slot{e->conv2.b, {D6}, 0, 0};
+    e->epos = e->take((size_t)TENC * D);
+    e->slots["model.encoder.embed_positions.weight"] = Slot{e->epos, {TENC, D6}, 0, 0};
+    e->encv.resize(d->enc_layers);
+    for (int i = 0; i < d->enc_layers; i++) {
+        std::string p = "model.encoder.layers." + std::to_string(i);
+        EncLayer& L = e->encv[i];
+        ln(L.ln1, p + ".self_attn_layer_norm");
+        qkv(L.qkv, p + ".self_attn");
+        lin(L.o, p + ".self_attn.out_proj", D, D);
+        ln(L.ln2, p + ".final_layer_norm");
+        lin(L.fc1, p + ".fc1", F, D);
+        lin(L.fc2, p + ".fc2", D, F);
+    }
+    ln(e->eln, "model.encoder.layer_norm");
+    e->decv.resize(nl);
+    // every decoder layer's cross k/v projection fused: [nl][k|v][D] rows of D, bias [0 | v bias] per layer
+    e->xkv.w = e->take((size_t)nl * 2 * D * D);
+    e->xkv.b = e->take((size_t)nl * 2 * D);
+    for (int i = 0; i < nl; i++) {
+        std::string p = "model.decoder.layers." + std::to_string(i);
+        DecLayer& L = e->decv[i];
+        ln(L.ln1, p + ".self_attn_layer_norm");
+        qkv(L.qkv, p + ".self_attn");
+        lin(L.o, p + ".self_attn.out_proj", D, D);
+        ln(L.lnx, p + ".encoder_attn_layer_norm");
+        lin(L.xq, p + ".encoder_attn.q_proj", D, D);
+        lin(L.xo, p + ".encoder_attn.out_proj", D, D);
+        ln(L.ln3, p + ".final_layer_norm");
+        lin(L.fc1, p + ".fc1", F, D);
+        lin(L.fc2, p + ".fc2", D, F);
+        e->slots[p + ".encoder_attn.k_proj.weight"] = Slot{e->xkv.w + (size_t)(2 * i) * D * D, {D6, D6}, 0, 0};
+        e->slots[p + ".encoder_attn.v_proj.weight"] = Slot{e->xkv.w + (size_t)(2 * i + 1) * D * D, {D6, D6}, 0, 0};
+        e->slots[p + ".encoder_attn.v_proj.bias"] = Slot{e->xkv.b + (size_t)(2 * i + 1) * D, {D6}, 0, 0};
+    }
+    e->emb = e->take((size_t)V * D);
+    e->slots["model.decoder.embed_tokens.weight"] = Slot{e->emb, {V, D6}, 0, 0};
+    e->dpos = e->take((size_t)mt * D);
+    e->slots["model.decoder.embed_positions.weight"] = Slot{e->dpos, {mt, D6}, 0, 0};
+    ln(e->dln, "model.decoder.layer_norm");
+    if (e->arena_used > e->arena_elems) return fail(mz_fail(MZ_ERR_STATE, "weight arena too small"));
+
+    // scratch
+    const size_t G = eg, B = bmax;
+    int r = 0;
+    if ((r = e->alloc(&e->mel, G * d->n_mels * NFR)) || (r = e->alloc(&e->melT, G * NFR * d->n_mels)) ||
+        (r = e->alloc(&e->h1, G * NFR * D)) || (r = e->alloc(&e->ex, G * TENC * D)) ||
+        (r = e->alloc(&e->hb, G * TENC * D)) || (r = e->alloc(&e->qkvh, G * 3 * nh * (size_t)TPAD * HD)) ||
+        (r = e->alloc(&e->att, G * TENC * D)) || (r = e->alloc(&e->ff, G * TENC * F)))
+        return fail(r);
+    if ((r = e->alloc(&e->xkvbuf, B * nl * 2 * nh * (size_t)TPAD * HD)) || (r = e->alloc(&e->tok, B * mt)) ||
+        (r = e->alloc(&e->done, B)) || (r = e->alloc(&e->ctr, 4)) || (r = e->alloc(&e->x, B * D)) ||
+        (r = e->alloc(&e->q, B * D)) || (r = e->alloc(&e->h, B * D)) || (r = e->alloc(&e->datt, B * D)) ||
+        (r = e->alloc(&e->dff, B * F)) || (r = e->alloc(&e->kc, (size_t)nl * B * nh * mt * HD)) ||
+        (r = e->alloc(&e->vct, (size_t)nl * B * nh * HD * mt)) || (r = e->alloc(&e->logits, B * V)) ||
+        (r = e->alloc(&e->align, B * mt * e->na * (size_t)TENC)) ||
+        (r = e->alloc(&e->xpart, B * nh * ((TENC + XCHUNK - 1) / XCHUNK) * 66)) || (r = e->alloc(&e->xcnt, B * nh)) ||
+        (r = e->alloc(&e->acnt, 4)) || (r = e->alloc(&e->sal, B * e->na * (size_t)TPAD)) ||
+        (r = e->alloc(&e->aslot, (size_t)nl * nh)) || (r = e->alloc(&e->sup, V)) || (r = e->alloc(&e->sup_lang, V)))
+        return fail(r);
+    // split-K partials: the largest ks * rows * n over the decoder products
+    size_t pe = 0;
+    for (auto nk : {std::pair<int, int>{D, D}, {D, F}}) pe = std::max(pe, (size_t)ksplit_for(nk.first, nk.second) * B * nk.first);
+    e->part_elems = pe;
+    if ((r = e->alloc(&e->part, pe))) return fail(r);
+
+    // masks and alignment slots (src/model.rs:411-425)
+    std::vector<unsigned char> supm(V, 0), langm(V, 1);
+    for (int i = 0; i < g->n_suppress; i++) {
+        int t = g->suppress[i];
+        if (t < 0 || t >= V) return fail(mz_fail(MZ_ERR_ARG, "suppress token %d out of range", t));
+        supm[t] = 1;
+    }
+    for (int i = 0; i < g->n_langs; i++) {
+        int t = g->lang_tokens[i];
+        if (t < 0 || t >= V) return fail(mz_fail(MZ_ERR_ARG, "language token %d out of range", t));
+        langm[t] = 0;
+    }
+    std::vector<int> sl((size_t)nl * nh, -1);
+    for (int s = 0; s < e->na; s++) sl[(size_t)e->align_heads[2 * s] * nh + e->align_heads[2 * s + 1]] = s;
+    if ((r = mz_upload(c, (uint64_t)(uintptr_t)e->sup, supm.data(), V)) ||
+        (r = mz_upload(c, (uint64_t)(uintptr_t)e->sup_lang, langm.data(), V)) ||
+        (r = mz_upload(c, (uint64_t)(uintptr_t)e->aslot, sl.data(), sl.size() * 4)))
+        return fail(r);
+    *out = e;
+    return MZ_OK;
+}
+
+extern "C" int mz_engine_put(mz_engine* e, const char* name, int dtype, const void* data, const int64_t* shape,
+                             int ndim) {
+    if (!e || !name || !data || (!shape && ndim)) return mz_fail(MZ_ERR_ARG, "mz_engine_put: null argument");
+    auto it = e->slots.find(name);
+    if (it == e->slots.end()) return MZ_OK;  // tensors the engine does not use (e.g. the tied proj_out) are ignored
+    const Slot& s = it->second;
+    if ((int)s.shape.size() != ndim || !std::equal(s.shape.begin(), s.shape.end(), shape)) {
+        std::string want, got;
+        for (auto v : s.shape) want += std::to_string(v) + ",";
+        for (int i = 0; i < ndim; i++) got += std::to_string(shape[i]) + ",";
+        return mz_fail(MZ_ERR_ARG, "%s has shape [%s], expected [%s]", name, got.c_str(), want.c_str());
+    }
+    if (dtype != MZ_DT_F16 && dtype != MZ_DT_F32) return mz_fail(MZ_ERR_ARG, "%s: unsupported dtype %d", name, dtype);
+    size_t n = 1;
+    for (auto v : s.shape) n *= (size_t)v;
+    std::vector<uint16_t> h16(n);
+    if (dtype == MZ_DT_F16) {
+        std::memcpy(h16.data(), data, n * 2);
+    } else {
+        const float* f = (const float*)data;
+        for (size_t i = 0; i < n; i++) h16[i] = mz_f2h_host(f[i]);
+    }
+    if (s.kind == 1) {  // conv weight [co][ci][3] -> [co][kpad], column tap * ci_n + ci
+        const size_t co = s.shape[0], ci = s.shape[1];
+        std::vector<uint16_t> w((size_t)co * s.kpad, 0);
+        for (size_t o = 0; o < co; o++)
+            for (size_t i = 0; i < ci; i++)
+                for (size_t t = 0; t < 3; t++) w[o * s.kpad + t * ci + i] = h16[(o * ci + i) * 3 + t];
+        h16.swap(w);
+    }
+    if (int r = mz_upload(e->c, (uint64_t)(uintptr_t)s.dst, h16.data(), h16.size() * 2)) return r;
+    e->placed.insert(name);
+    return MZ_OK;
+}
+
+extern "C" int mz_engine_finish(mz_engine* e) {
+    if (!e) return mz_fail(MZ_ERR_ARG, "mz_engine_finish: null engine");
+    for (auto& kv : e->slots)
+        if (!e->placed.count(kv.first)) return mz_fail(MZ_ERR_STATE, "model tensor %s was not provided", kv.first.c_str());
+    e->loaded = true;
+    return MZ_OK;
+}
+
+extern "C" int mz_engine_set_trace(mz_engine* e, int on) {
+    if (!e) return mz_fail(MZ_ERR_ARG, "mz_engine_set_trace: null engine");
+    if (on && !e->trace) {
+        if (int r = e->alloc(&e->trace, (size_t)e->dm.enc_layers * e->eg * TENC * e->dm.d)) return r;
+    }
+    e->trace_on = on != 0;
+    return MZ_OK;
+}
+
+#define TRY(expr, what)                                     \
+    do {                                                    \
+        if (int _r = mz_hip((expr), what)) return _r;       \
+    } while (0)
+
+extern "C" int mz_engine_encode(mz_engine* e, const float* mels, int n, int slot0) {
+    if (!e || !mels) return mz_fail(MZ_ERR_ARG, "mz_engine_encode: null argument");
+    if (!e->loaded) return mz_fail(MZ_ERR_STATE, "mz_engine_encode: weights not loaded (mz_engine_finish)");
+    if (n <= 0 || n > e->eg || slot0 < 0 || slot0 + n > e->bmax)
+        return mz_fail(MZ_ERR_ARG, "mz_engine_encode: %d clips at slot %d (enc group %d, bmax %d)", n, slot0, e->eg, e->bmax);
+    hipStream_t s = e->c->stream;
+    const int D = e->dm.d, nm = e->dm.n_mels, nh = e->dm.nh, F = e->dm.ff, nl = e->dm.dec_layers;
+    const int rows = n * TENC;
+    TRY(hipMemcpyAsync(e->mel, mels, (size_t)n * nm * NFR * 4, hipMemcpyHostToDevice, s), "mel upload");
+    TRY(mz_mel_transpose_launch(s, e->mel, e->melT, n, nm), "mel transpose");
+    // conv stem as implicit GEMMs (src/model.rs:552-558): GELU(conv1), GELU(conv2, stride 2) + positions
+    MzGemm g{};
+    g.A = e->melT;
+    g.W = e->conv1.w;
+    g.bias = e->conv1.b;
+    g.M = n * NFR;
+    g.N = D;
+    g.K = e->k1pad;
+    g.conv_cin = nm;
+    g.conv_tin = NFR;
+    g.conv_tout = NFR;
+    g.conv_stride = 1;
+    g.out = e->h1;
+    g.ldo = D;
+    TRY(mz_gemm_launch(s, ALOAD_CONV, EPI_GELU_F16, g), "conv1");
+    g = MzGemm{};
+    g.A = e->h1;
+    g.W = e->conv2.w;
+    g.bias = e->conv2.b;
+    g.M = rows;
+    g.N = D;
+    g.K = 3 * D;
+    g.conv_cin = D;
+    g.conv_tin = NFR;
+    g.conv_tout = TENC;
+    g.conv_stride = 2;
+    g.out = e->ex;
+    g.ldo = D;
+    g.pos = e->epos;
+    TRY(mz_gemm_launch(s, ALOAD_CONV, EPI_GELU_POS, g), "conv2");
+    TRY(mz_layernorm_launch(s, e->ex, D, e->encv[0].ln1.w, e->encv[0].ln1.b, e->hb, D, rows, D, EPS), "ln");
+    for (int i = 0; i < e->dm.enc_layers; i++) {
+        const EncLayer& L = e->encv[i];
+        if (e->trace_on)
+            TRY(hipMemcpyAsync(e->trace + (size_t)i * e->eg * TENC * D, e->ex, (size_t)rows * D * 4,
+                               hipMemcpyDeviceToDevice, s),
+                "trace");
+        g = MzGemm{};
+        g.A = e->hb;
+        g.lda = D;
+        g.W = L.qkv.w;
+        g.bias = L.qkv.b;
+        g.M = rows;
+        g.N = 3 * D;
+        g.K = D;
+        g.heads = e->qkvh;
+        g.blocks_per_clip = 3 * nh;
+        g.nh = nh;
+        g.kind = 3;
+        TRY(mz_gemm_launch(s, ALOAD_PLAIN, EPI_HEADS, g), "qkv");
+        TRY(mz_enc_attention_launch(s, e->qkvh, e->att, n, nh), "attention");
+        g = MzGemm{};
+        g.A = e->att;
+        g.lda = D;
+        g.W = L.o.w;
+        g.bias = L.o.b;
+        g.M = rows;
+        g.N = D;
+        g.K = D;
+        g.out = e->ex;
+        g.ldo = D;
+        TRY(mz_gemm_launch(s, ALOAD_PLAIN, EPI_RESID_F32, g), "out-proj");
+        TRY(mz_layernorm_launch(s, e->ex, D, L.ln2.w, L.ln2.b, e->hb, D, rows, D, EPS), "ln2");
+        g.A = e->hb;
+        g.W = L.fc1.w;
+        g.bias = L.fc1.b;
+        g.N = F;
+        g.out = e->ff;
+        g.ldo = F;
+        TRY(mz_gemm_launch(s, ALOAD_PLAIN, EPI_GELU_F16, g), "fc1");
+        g.A = e->ff;
+        g.lda = F;
+        g.W = L.fc2.w;
+        g.bias = L.fc2.b;
+        g.N = D;
+        g.K = F;
+        g.out = e->ex;
+        g.ldo = D;
+        TRY(mz_gemm_launch(s, ALOAD_PLAIN, EPI_RESID_F32, g), "fc2");
+        const Ln& nx = i + 1 < e->dm.enc_layers ? e->encv[i + 1].ln1 : e->eln;  // the last one is the final LN
+        TRY(mz_layernorm_launch(s, e->ex, D, nx.w, nx.b, e->hb, D, rows, D, EPS), "ln");
+    }
+    // cross k/v of every decoder layer for the clips' slots (src/model.rs:614-623)
+    g = MzGemm{};
+    g.A = e->hb;
+    g.lda = D;
+    g.W = e->xkv.w;
+    g.bias = e->xkv.b;
+    g.M = rows;
+    g.N = nl * 2 * D;
+    g.K = D;
+    g.heads = e->xkvbuf;
+    g.blocks_per_clip = nl * 2 * nh;
+    g.nh = nh;
+    g.kind = 2;
+    g.slot0 = slot0;
+    TRY(mz_gemm_launch(s, ALOAD_PLAIN, EPI_HEADS, g), "cross k/v");
+    return MZ_OK;
+}
+
+extern "C" int mz_engine_reset(mz_engine* e, const int32_t* prompts, int n, int prompt_len) {
+    if (!e || !prompts) return mz_fail(MZ_ERR_ARG, "mz_engine_reset: null argument");
+    if (n <= 0 || n > e->bmax || prompt_len <= 0 || prompt_len >= e->dm.max_t)
+        return mz_fail(MZ_ERR_ARG, "mz_engine_reset: %d rows, prompt of %d", n, prompt_len);
+    const int mt = e->dm.max_t;
+    std::vector<int32_t> t((size_t)n * mt, 0);
+    for (int b = 0; b < n; b++)
+        for (int i = 0; i < prompt_len; i++) {
+            int v = prompts[(size_t)b * prompt_len + i];
+            if (v < 0 || v >= e->dm.vocab) return mz_fail(MZ_ERR_ARG, "prompt token %d out of range", v);
+            t[(size_t)b * mt + i] = v;
+        }
+    std::vector<int32_t> zeros(std::max(n, 4), 0);
+    if (int r = mz_upload(e->c, (uint64_t)(uintptr_t)e->tok, t.data(), t.size() * 4)) return r;
+    if (int r = mz_upload(e->c, (uint64_t)(uintptr_t)e->done, zeros.data(), (size_t)n * 4)) return r;
+    return mz_upload(e->c, (uint64_t)(uintptr_t)e->ctr, zeros.data(), 16);
+}
+
+static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
+    hipStream_t s = e->c->stream;
+    const int D = e->dm.d, F = e->dm.ff, nh = e->dm.nh, nl = e->dm.dec_layers, mt = e->dm.max_t, V = e->dm.vocab;
+    const long blk = (long)TPAD * HD;
+    TRY(mz_dec_embed_ln_launch(s, e->tok, e->ctr, e->emb, e->dpos, e->x, e->decv[0].ln1.w, e->decv[0].ln1.b, e->h, b, D,
+                               mt, EPS),
+        "embed");
+    auto gemm = [&](int epi, const f16* x, int ldx, const Lin& L, int N, int K, int ks, void* out, long ldo) {
+        MzDec g{};
+        g.x = x;
+        g.ldx = ldx;
+        g.W = L.w;
+        g.bias = L.b;
+        g.M = b;
+        g.N = N;
+        g.K = K;
+        g.ksplit = ks;
+        g.out = out;
+        g.ldo = ldo;
+        return mz_dec_gemm_launch(s, epi, g);
+    };
+    const int ks_dd = ksplit_for(D, D), ks_df = ksplit_for(D, F);
+    for (int i = 0; i < nl; i++) {
+        const DecLayer& L = e->decv[i];
+        f16* kc = e->kc + (size_t)i * e->bmax * nh * mt * HD;
+        f16* vct = e->vct + (size_t)i * e->bmax * nh * HD * mt;
+        {
+            MzDec g{};
+            g.x = e->h;
+            g.ldx = D;
+            g.W = L.qkv.w;
+            g.bias = L.qkv.b;
+            g.M = b;
+            g.N = 3 * D;
+            g.K = D;
+            g.ksplit = 1;
+            g.out = e->q;
+            g.ldo = D;
+            g.kc = kc;
+            g.vct = vct;
+            g.ctr = e->ctr;
+            g.maxT = mt;
+            g.d = D;
+            TRY(mz_dec_gemm_launch(s, DEPI_QKV, g), "dec qkv");
+        }
+        MzDecAttn a{};
+        a.q = e->q;
+        a.nq = 1;
+        a.k = kc;
+        a.vt = vct;
+        a.kv_b = (long)nh * mt * HD;
+        a.kv_h = (long)mt * HD;
+        a.vt_ld = mt;
+        a.L = -1;
+        a.ctr = e->ctr;
+        a.done = e->done;
+        a.out = e->datt;
+        a.B = b;
+        a.nh = nh;
+        a.d = D;
+        a.nsplit = 1;
+        a.chunk = rup(mt, 8);
+        TRY(mz_dec_attn_launch(s, a), "self attention");
+        TRY(gemm(DEPI_PARTIAL, e->datt, D, L.o, D, D, ks_dd, e->part, D), "dec out-proj");
+        TRY(mz_dec_add_ln_launch(s, e->x, e->part, ks_dd, (long)b * D, L.o.b, L.lnx.w, L.lnx.b, e->h, b, D, EPS), "add+ln");
+        TRY(gemm(DEPI_PARTIAL, e->h, D, L.xq, D, D, ks_dd, e->part, D), "dec cross q");
+        a = MzDecAttn{};
+        a.q = e->part;
+        a.nq = ks_dd;
+        a.qstride = (long)b * D;
+        a.qbias = L.xq.b;
+        a.k = e->xkvbuf + (size_t)(2 * i) * nh * blk;
+        a.vt = e->xkvbuf + (size_t)(2 * i + 1) * nh * blk;
+        a.kv_b = (long)nl * 2 * nh * blk;
+        a.kv_h = blk;
+        a.vt_ld = TPAD;
+        a.L = TENC;
+        a.ctr = e->ctr;
+        a.done = e->done;
+        a.out = e->datt;
+        a.B = b;
+        a.nh = nh;
+        a.d = D;
+        a.nsplit = (TENC + XCHUNK - 1) / XCHUNK;
+        a.chunk = XCHUNK;
+        a.part = e->xpart;
+        a.counter = e->xcnt;
+        a.aslot = e->aslot + (size_t)i * nh;
+        a.sal = e->sal;
+        a.align = e->align;
+        a.na = e->na;
+        a.maxT = mt;
+        TRY(mz_dec_attn_launch(s, a), "cross attention");
+        TRY(gemm(DEPI_PARTIAL, e->datt, D, L.xo, D, D, ks_dd, e->part, D), "dec cross out-proj");
+        TRY(mz_dec_add_ln_launch(s, e->x, e->part, ks_dd, (long)b * D, L.xo.b, L.ln3.w, L.ln3.b, e->h, b, D, EPS), "add+ln");
+        TRY(gemm(DEPI_GELU_F16, e->h, D, L.fc1, F, D, 1, e->dff, F), "dec fc1");
+        TRY(gemm(DEPI_PARTIAL, e->dff, F, L.fc2, D, F, ks_df, e->part, D), "dec fc2");
+        const Ln& nx = i + 1 < nl ? e->decv[i + 1].ln1 : e->dln;
+        TRY(mz_dec_add_ln_launch(s, e->x, e->part, ks_df, (long)b * D, L.fc2.b, nx.w, nx.b, e->h, b, D, EPS), "add+ln");
+    }
+    // tied LM head, then the greedy choice; its last block advances the position
+    Lin head{e->emb, nullptr};
+    TRY(gemm(DEPI_F32, e->h, D, head, V, D, 1, e->logits, V), "lm head");
+    TRY(mz_dec_argmax_launch(s, e->logits, V, lang ? e->sup_lang : e->sup, e->tok, e->done, e->ctr, e->acnt, b, mt,
+                             prompt_len, e->eos, lang ? -1 : e->bs1, lang ? -1 : e->bs2, 1),
+        "argmax");
+    return MZ_OK;
+}
+
+extern "C" int mz_engine_step(mz_engine* e, int b, int lang, int prompt_len) {
+    if (!e) return mz_fail(MZ_ERR_ARG, "mz_engine_step: null engine");
+    if (!e->loaded) return mz_fail(MZ_ERR_STATE, "mz_engine_step: weights not loaded");
+    if (b <= 0 || b > e->bmax) return mz_fail(MZ_ERR_ARG, "mz_engine_step: %d rows (bmax %d)", b, e->bmax);
+    return step_impl(e, b, lang, prompt_len);
+}
+
+extern "C" int mz_engine_detect(mz_engine* e, int b, int32_t* langs) {
+    if (!e || !langs) return mz_fail(MZ_ERR_ARG, "mz_engine_detect: null argument");
+    if (int r = mz_engine_step(e, b, 1, 1)) return r;
+    const int mt = e->dm.max_t;
+    std::vector<int32_t> t((size_t)b * mt);
+    if (int r = mz_download(e->c, t.data(), (uint64_t)(uintptr_t)e->tok, t.size() * 4)) return r;
+    for (int i = 0; i < b; i++) langs[i] = t[(size_t)i * mt + 1];
+    return MZ_OK;
+}
+
+extern "C" int mz_engine_capture(mz_engine* e, int b, int prompt_len) {
+    if (!e) return mz_fail(MZ_ERR_ARG, "mz_engine_capture: null engine");
+    if (!e->loaded) return mz_fail(MZ_ERR_STATE, "mz_engine_capture: weights not loaded");
+    if (b <= 0 || b > e->bmax) return mz_fail(MZ_ERR_ARG, "mz_engine_capture: %d rows", b);
+    if (e->graph) {
+        mz_graph_free(e->graph);
+        e->graph = nullptr;
+    }
+    if (int r = mz_graph_begin(e->c)) return r;
+    int rs = step_impl(e, b, 0, prompt_len);
+    mz_graph* g = nullptr;
+    int re = mz_graph_end(e->c, &g);
+    if (rs) {
+        mz_graph_free(g);
+        return rs;
+    }
+    if (re) return re;
+    e->graph = g;
+    e->graph_b = b;
+    e->graph_np = prompt_len;
+    return MZ_OK;
+}
+
+extern "C" int mz_engine_replay(mz_engine* e) {
+    if (!e || !e->graph) return mz_fail(MZ_ERR_STATE, "mz_engine_replay: no captured step");
+    return mz_graph_launch(e->c, e->graph);
+}
+
+extern "C" int mz_engine_buffer(mz_engine* e, int which, uint64_t* dptr, size_t* bytes) {
+    if (!e || !dptr || !bytes) return mz_fail(MZ_ERR_ARG, "mz_engine_buffer: null argument");
+    const size_t D = e->dm.d, B = e->bmax, mt = e->dm.max_t, G = e->eg;
+    void* p = nullptr;
+    size_t n = 0;
+    switch (which) {
+        case MZ_BUF_TOK: p = e->tok, n = B * mt * 4; break;
+        case MZ_BUF_DONE: p = e->done, n = B * 4; break;
+        case MZ_BUF_CTR: p = e->ctr, n = 16; break;
+        case MZ_BUF_ALIGN: p = e->align, n = B * mt * e->na * TENC * 2; break;
+        case MZ_BUF_ENC_OUT: p = e->hb, n = G * TENC * D * 2; break;
+        case MZ_BUF_LOGITS: p = e->logits, n = B * e->dm.vocab * 4; break;
+        case MZ_BUF_TRACE:
+            if (!e->trace) return mz_fail(MZ_ERR_STATE, "trace not enabled");
+            p = e->trace, n = (size_t)e->dm.enc_layers * G * TENC * D * 4;
+            break;
+        case MZ_BUF_XKV: p = e->xkvbuf, n = B * e->dm.dec_layers * 2 * e->dm.nh * (size_t)TPAD * HD * 2; break;
+        case MZ_BUF_DEC_X: p = e->x, n = B * D * 4; break;
+        case MZ_BUF_ENC_X: p = e->ex, n = G * TENC * D * 4; break;
+        default: return mz_fail(MZ_ERR_ARG, "unknown engine buffer %d", which);
+    }
+    *dptr = (uint64_t)(uintptr_t)p;
+    *bytes = n;
+    return MZ_OK;
+}
+
+extern "C" int mz_engine_read(mz_engine* e, int which, void* dst, size_t offset, size_t bytes) {
+    uint64_t p;
+    size_t n;
+    if (int r = mz_engine_buffer(e, which, &p, &n)) return r;
+    if (offset + bytes > n) return mz_fail(MZ_ERR_ARG, "mz_engine_read: %zu bytes at %zu of %zu", bytes, offset, n);
+    return mz_download(e->c, dst, p + offset, bytes);
+}
+
+extern "C" int mz_engine_free(mz_engine* e) {
+    if (!e) return MZ_OK;
+    if (e->graph) mz_graph_free(e->graph);
+    hipStreamSynchronize(e->c->stream);
+    for (void* p : {(void*)e->arena, (void*)e->mel, (void*)e->melT, (void*)e->h1, (void*)e->ex, (void*)e->hb,
+                    (void*)e->qkvh, (void*)e->att, (void*)e->ff, (void*)e->trace, (void*)e->xkvbuf, (void*)e->tok,
+                    (void*)e->done, (void*)e->ctr, (void*)e->x, (void*)e->q, (void*)e->h, (void*)e->datt,
+                    (void*)e->dff, (void*)e->kc, (void*)e->vct, (void*)e->logits, (void*)e->align, (void*)e->xpart,
+                    (void*)e->xcnt, (void*)e->acnt, (void*)e->sal, (void*)e->aslot, (void*)e->sup, (void*)e->sup_lang,
+                    (void*)e->part})
+        if (p) mz_free(e->c, (uint64_t)(uintptr_t)p);
+    delete e;
+    return MZ_OK;
+}
+
+// ------------------------------------------------------------------ batch transcription (src/transcribe.rs:104-167)
+
+extern "C" int mz_transcribe(mz_engine* e, const float* mels, const int32_t* frames, int n, const int32_t* prompt,
+                             int prompt_len, int detect, int use_graph, int max_new, int half_align, int32_t* seq,
+                             int32_t* seq_len, float* ts, int32_t* langs, mz_times* times) {
+    using clk = std::chrono::steady_clock;
+    if (!e || !mels || !frames || !prompt || !seq || !seq_len || !ts || !langs)
+        return mz_fail(MZ_ERR_ARG, "mz_transcribe: null argument");
+    if (n <= 0 || n > e->bmax) return mz_fail(MZ_ERR_ARG, "mz_transcribe: %d clips (bmax %d)", n, e->bmax);
+    const int mt = e->dm.max_t, nm = e->dm.n_mels, eos = e->eos, np = prompt_len;
+    auto sec = [](clk::time_point a) { return std::chrono::duration<double>(clk::now() - a).count(); };
+    mz_times tm{};
+
+    auto t0 = clk::now();
+    for (int g0 = 0; g0 < n; g0 += e->eg) {
+        const int gn = std::min(e->eg, n - g0);
+        if (int r = mz_engine_encode(e, mels + (size_t)g0 * nm * NFR, gn, g0)) return r;
+    }
+    if (int r = mz_sync(e->c)) return r;
+    tm.enc = sec(t0);
+
+    t0 = clk::now();
+    std::vector<int32_t> pr((size_t)n * np);
+    for (int b = 0; b < n; b++)
+        for (int i = 0; i < np; i++) pr[(size_t)b * np + i] = prompt[i];
+    if (int r = mz_engine_reset(e, pr.data(), n, np)) return r;
+    std::vector<int32_t> lg(n, np > 1 ? prompt[1] : -1);
+    int steps = 0;
+    if (detect) {
+        if (int r = mz_engine_detect(e, n, lg.data())) return r;
+        steps = 1;
+    }
+    const int limit = max_new > 0 ? std::min(mt - 1, np - 1 + max_new) : mt - 1;
+    if (use_graph) {
+        if (!e->graph || e->graph_b != n || e->graph_np != np)
+            if (int r = mz_engine_capture(e, n, np)) return r;
+    }
+    std::vector<int32_t> dn(n);
+    while (steps < limit) {
+        if (int r = use_graph ? mz_engine_replay(e) : step_impl(e, n, 0, np)) return r;
+        steps++;
+        if (steps % 8 == 0 && steps >= np) {
+            if (int r = mz_download(e->c, dn.data(), (uint64_t)(uintptr_t)e->done, (size_t)n * 4)) return r;
+            if (std::all_of(dn.begin(), dn.end(), [](int v) { return v != 0; })) break;
+        }
+    }
+    if (int r = mz_sync(e->c)) return r;
+    tm.dec = sec(t0);
+    tm.steps = steps;
+
+    t0 = clk::now();
+    std::vector<int32_t> toks((size_t)n * mt);
+    if (int r = mz_download(e->c, toks.data(), (uint64_t)(uintptr_t)e->tok, toks.size() * 4)) return r;
+    const size_t row = (size_t)e->na * TENC;
+    std::vector<uint16_t> wh;
+    std::vector<float> w, jt;
+    for (int c = 0; c < n; c++) {
+        const int32_t* t = &toks[(size_t)c * mt];
+        int n_seq = std::min(steps + 1, mt);
+        for (int k = np; k < mt; k++)
+            if (t[k] == eos) {
+                n_seq = std::min(k + 1, mt);
+                break;
+            }
+        n_seq = std::min(n_seq, steps + 1);
+        for (int k = 0; k < mt; k++) seq[(size_t)c * mt + k] = k < n_seq ? t[k] : 0;
+        seq_len[c] = n_seq;
+        float* tc = ts + (size_t)c * mt;
+        std::fill(tc, tc + mt, 0.f);
+        const int rows = std::max(n_seq - 1 - np, 0);
+        if (rows > 0) {
+            wh.resize((size_t)rows * row);
+            if (int r = mz_download(e->c, wh.data(), (uint64_t)(uintptr_t)(e->align + ((size_t)c * mt + np) * row),
+                                    wh.size() * 2))
+                return r;
+            w.resize(wh.size());
+            for (size_t k = 0; k < wh.size(); k++) w[k] = mz_h2f_host(wh[k]);
+            jt.resize(rows);
+            if (int r = mz_jump_times(w.data(), rows, e->na, TENC, frames[c] / 2, 7, half_align, jt.data())) return r;
+            for (int k = 0; k < rows; k++) tc[np + k] = jt[k];
+            tc[n_seq - 1] = jt[rows - 1];
+        }
+        langs[c] = lg[c];
+    }
+    tm.post = sec(t0);
+    if (times) *times = tm;
+    return MZ_OK;
+}

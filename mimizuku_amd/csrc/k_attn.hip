@@ -1,0 +1,152 @@
+// Encoder self-attention for head_dim 64 on the gfx950 matrix cores (non-causal, 1500 keys, scale 1/8), replacing
+// kernels/whisper.cu:168-299 (enc_flash). softmax(Q K^T / 8) V with fp32 scores and online softmax, P rounded to
+// fp16 for the P.V product, O / l rounded to fp16 (the SDPA arithmetic the reference follows, whisper.cu:3-4).
+//
+// Work: one block per (256 queries, head, clip) = 4 waves x 2 sets of 32 queries. K and V^T tiles of 64 keys are
+// staged in LDS (double buffered, register prefetch) and shared by the 4 waves. Scores are computed transposed,
+// S^T = K Q^T (32x32x16 MFMA), so each lane owns one query column: the running max / sum and the rescale of O are
+// per lane, and the only cross-lane step is one swap with lane l ^ 32. K rows are stored in LDS with bits 2 and 3
+// of the key index swapped, which makes each lane's 16 scores two runs of 8 consecutive keys: the scores, rounded
+// to fp16, are directly the B operand of O^T = V^T P^T, and V^T (written transposed by the QKV GEMM) is read with
+// 16-byte LDS loads. exp uses v_exp_f32 (exp2) with log2(e) folded into the scale.
+#include "mz_common.h"
+#include "mz_kernels.h"
+
+namespace {
+
+constexpr int KP = 72;  // LDS row pitch in halves (144 B): conflict-free 16-byte fragment reads
+constexpr int QB = 256; // queries per block
+constexpr int NT = MZ_TPAD / 64;  // key tiles (the last one holds keys 1472..1535, valid < 1500)
+
+__device__ __forceinline__ int swap23(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) enc_attn_kernel(const f16* __restrict__ qkvh, f16* __restrict__ out, int nh) {
+    __shared__ __attribute__((aligned(16))) f16 sK[2][64 * KP];
+    __shared__ __attribute__((aligned(16))) f16 sV[2][64 * KP];
+
+    const int head = blockIdx.y, g = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, lh = lane >> 5;
+    const long blk = (long)MZ_TPAD * MZ_HD;
+    const f16* Q = qkvh + ((long)g * 3 * nh + head) * blk;
+    const f16* K = Q + (long)nh * blk;
+    const f16* Vt = Q + 2L * nh * blk;
+    const int d = nh * MZ_HD;
+
+    // query fragments (B operand of S^T): query row, dims 16c + 8 lh .. + 8
+    const int q0 = blockIdx.x * QB + wave * 64;
+    f16x8 qf[2][4];
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) qf[s][c] = ld8(Q + (long)(q0 + s * 32 + lr) * MZ_HD + 16 * c + 8 * lh);
+
+    // this thread's two K chunks and two V^T chunks of a tile
+    const int c0 = tid, c1 = tid + 256;
+    const int kr0 = c0 >> 3, kr1 = c1 >> 3, cc = (tid & 7) * 8;
+    f16x8 pk0, pk1, pv0, pv1;
+    auto gload = [&](int kt) {
+        pk0 = ld8(K + (long)(kt * 64 + kr0) * MZ_HD + cc);
+        pk1 = ld8(K + (long)(kt * 64 + kr1) * MZ_HD + cc);
+        pv0 = ld8(Vt + (long)kr0 * MZ_TPAD + kt * 64 + cc);
+        pv1 = ld8(Vt + (long)kr1 * MZ_TPAD + kt * 64 + cc);
+    };
+    auto lstore = [&](int buf) {
+        *(f16x8*)&sK[buf][swap23(kr0) * KP + cc] = pk0;
+        *(f16x8*)&sK[buf][swap23(kr1) * KP + cc] = pk1;
+        *(f16x8*)&sV[buf][kr0 * KP + cc] = pv0;
+        *(f16x8*)&sV[buf][kr1 * KP + cc] = pv1;
+    };
+
+    const float cs = 0.125f * 1.4426950408889634f;  // scale * log2(e)
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+    f32x16 o[2][2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) o[s][0] = o[s][1] = f32x16{};
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < NT; kt++) {
+        const int buf = kt & 1;
+        if (kt + 1 < NT) gload(kt + 1);
+#pragma unroll
+        for (int ss = 0; ss < 2; ss++) {  // 32-key halves of the tile
+            f16x8 kf[4], vf[2][2];
+#pragma unroll
+            for (int c = 0; c < 4; c++) kf[c] = *(const f16x8*)&sK[buf][(32 * ss + lr) * KP + 16 * c + 8 * lh];
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int c = 0; c < 2; c++)
+                    vf[t][c] = *(const f16x8*)&sV[buf][(32 * t + lr) * KP + 32 * ss + 16 * c + 8 * lh];
+#pragma unroll
+            for (int qs = 0; qs < 2; qs++) {
+                f32x16 sc = {};
+#pragma unroll
+                for (int c = 0; c < 4; c++) sc = mfma32(kf[c], qf[qs][c], sc);
+                if (kt == NT - 1) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        int key = kt * 64 + 32 * ss + 16 * (r >> 3) + 8 * lh + (r & 7);
+                        if (key >= MZ_TENC) sc[r] = -INFINITY;
+                    }
+                }
+                float mx = sc[0];
+#pragma unroll
+                for (int r = 1; r < 16; r++) mx = fmaxf(mx, sc[r]);
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                const float mnew = fmaxf(m[qs], mx * cs);
+                const float corr = __builtin_amdgcn_exp2f(m[qs] - mnew);
+                m[qs] = mnew;
+                l[qs] *= corr;
+                if (__ballot(corr != 1.f)) {
+#pragma unroll
+                    for (int t = 0; t < 2; t++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) o[qs][t][r] *= corr;
+                }
+                f16x8 pf[2];
+                float ls = 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    float pr = __builtin_amdgcn_exp2f(fmaf(sc[r], cs, -mnew));
+                    ls += pr;
+                    pf[r >> 3][r & 7] = (f16)pr;
+                }
+                l[qs] += ls;
+#pragma unroll
+                for (int t = 0; t < 2; t++)
+#pragma unroll
+                    for (int c = 0; c < 2; c++) o[qs][t] = mfma32(vf[t][c], pf[c], o[qs][t]);
+            }
+        }
+        if (kt + 1 < NT) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int qs = 0; qs < 2; qs++) {
+        const float lt = l[qs] + __shfl_xor(l[qs], 32);
+        const float inv = 1.f / lt;
+        const int q = q0 + qs * 32 + lr;
+        if (q >= MZ_TENC) continue;
+        f16* dst = out + ((long)g * MZ_TENC + q) * d + head * MZ_HD;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; r4++) {
+                const int dim = 32 * t + 8 * r4 + 4 * lh;
+                st4(dst + dim, o[qs][t][4 * r4] * inv, o[qs][t][4 * r4 + 1] * inv, o[qs][t][4 * r4 + 2] * inv,
+                    o[qs][t][4 * r4 + 3] * inv);
+            }
+    }
+}
+
+}  // namespace
+
+hipError_t mz_enc_attention_launch(hipStream_t s, const f16* qkvh, f16* out, int G, int nh) {
+    if (G <= 0 || nh <= 0) return hipErrorInvalidValue;
+    dim3 grid((MZ_TENC + QB - 1) / QB, nh, G);
+    hipLaunchKernelGGL(enc_attn_kernel, grid, dim3(256), 0, s, qkvh, out, nh);
+    return hipGetLastError();
+}

@@ -1,0 +1,117 @@
+// Host-side launchers of the gfx950 kernels (internal to libmimizuku_amd; the C ABI is include/mimizuku.h).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+typedef _Float16 f16;
+
+// ---------------------------------------------------------------- tiled MFMA GEMM (encoder sizes)
+// C[m][n] = sum_k A[m][k] W[n][k] (+ bias[n]), fp16 operands, fp32 accumulation, K a multiple of 64.
+enum MzALoad { ALOAD_PLAIN = 0, ALOAD_CONV = 1 };
+enum MzEpi {
+    EPI_F16 = 0,        // out f16 [M][ldo] = acc + bias
+    EPI_GELU_F16 = 1,   // out f16 [M][ldo] = gelu(acc + bias)
+    EPI_RESID_F32 = 2,  // out f32 [M][ldo] += acc + bias        (residual add fused into the producing GEMM)
+    EPI_GELU_POS = 3,   // out f32 [M][ldo] = gelu(acc + bias) + pos[m % 1500][n]   (conv2 -> residual stream)
+    EPI_HEADS = 4,      // head-major scatter: K-like blocks [1536][64], V-like blocks transposed [64][1536]
+};
+
+struct MzGemm {
+    const f16* A;
+    long lda;
+    const f16* W;  // [N][K] row-major
+    const f16* bias;  // [N] or null
+    int M, N, K;
+    // ALOAD_CONV: A[g * tout + t][tap * cin + ci] = src[(g * tin + stride * t + tap - 1) * cin + ci], zero outside
+    int conv_cin, conv_tin, conv_tout, conv_stride;
+    // epilogues
+    void* out;
+    long ldo;
+    const f16* pos;
+    // EPI_HEADS: column n belongs to 64-wide block blk = n / 64 and row m = g * 1500 + t to clip g; the block's
+    // 1536 x 64 tile lives at heads + ((slot0 + g) * blocks_per_clip + blk) * 1536 * 64. kind 3: blocks ordered
+    // [q|k|v][head], kind 2: [layer][k|v][head]; the last member of each group (v) is stored transposed [64][1536].
+    f16* heads;
+    int blocks_per_clip, nh, kind, slot0;
+};
+hipError_t mz_gemm_launch(hipStream_t s, int aload, int epi, const MzGemm& g);
+
+// ---------------------------------------------------------------- encoder attention
+// qkvh: [G][3][nh] tiles of 1536 x 64 halves (q, k row-major [t][64]; v transposed [64][t]; t >= 1500 zero);
+// out: [G * 1500][nh * 64]
+hipError_t mz_enc_attention_launch(hipStream_t s, const f16* qkvh, f16* out, int G, int nh);
+
+// ---------------------------------------------------------------- norms and small encoder kernels
+// y[r] = LN(x[r]) (fp32 in, fp16 out), rows of dim (dim % 128 == 0, dim <= 2048)
+hipError_t mz_layernorm_launch(hipStream_t s, const float* x, long ldx, const f16* w, const f16* b, f16* y, long ldy,
+                               int rows, int dim, float eps);
+// x[r] += d[r] (f16), then y[r] = LN(x[r])
+hipError_t mz_add_layernorm_launch(hipStream_t s, float* x, const f16* d, const f16* w, const f16* b, f16* y, int rows,
+                                   int dim, float eps);
+// mel f32 [G][nm][3000] -> melT f16 [G][3000][nm]
+hipError_t mz_mel_transpose_launch(hipStream_t s, const float* mel, f16* melT, int G, int nm);
+
+// ---------------------------------------------------------------- decoder step
+// skinny GEMM for decode batches: rows m < M of x (f16, row stride ldx, M <= 32 per m-tile) times W[N][K]
+enum MzDecEpi {
+    DEPI_PARTIAL = 0,  // part[ks][m][n] (f32), ks = blockIdx.y (split-K)
+    DEPI_GELU_F16 = 1, // out f16 [m][ldo] = gelu(acc + bias)
+    DEPI_F32 = 2,      // out f32 [m][ldo] = acc (+ bias)
+    DEPI_QKV = 3,      // q -> qout f32 [m][d] (+bias); k, v (+bias) -> self cache at position ctr[0]
+    DEPI_F16 = 4,      // out f16 [m][ldo] = acc + bias
+};
+struct MzDec {
+    const f16* x;
+    long ldx;
+    const f16* W;
+    const f16* bias;
+    int M, N, K, ksplit;
+    void* out;
+    long ldo;
+    // DEPI_QKV
+    f16* kc;   // [bmax][nh][maxT][64] of this layer
+    f16* vct;  // [bmax][nh][64][maxT] of this layer
+    const int* ctr;
+    int maxT, d;
+};
+hipError_t mz_dec_gemm_launch(hipStream_t s, int epi, const MzDec& g);
+
+struct MzDecAttn {
+    // query: sum over nq slices of q[s * qstride + b * d + head * 64 + i] (+ qbias), scaled by 1/8
+    const float* q;
+    int nq;
+    long qstride;
+    const f16* qbias;
+    // keys of (b, head): k + b * kv_b + head * kv_h, rows of 64 halves; V^T likewise at vt, rows of vt_ld keys
+    const f16* k;
+    const f16* vt;
+    long kv_b, kv_h;   // element strides of a row b and a head (same for k and vt)
+    int vt_ld;         // keys per row of V^T
+    int L;             // keys (cross) or -1: ctr[0] + 1 (self)
+    const int* ctr;
+    const int* done;
+    f16* out;          // [B][d]
+    int B, nh, d;
+    int nsplit, chunk;  // key chunks per (b, head)
+    // split combine scratch
+    float* part;        // [B * nh][nsplit][66]
+    unsigned* counter;  // [B * nh]
+    // alignment-head capture (cross only, may be null)
+    const int* aslot;   // [nl * nh] for this layer: slot or -1 (already offset to the layer)
+    float* sal;         // [B][na][1536] raw scores
+    f16* align;         // [bmax][maxT][na][1500]
+    int na, maxT;
+};
+hipError_t mz_dec_attn_launch(hipStream_t s, const MzDecAttn& a);
+
+// x[b] += sum_s parts[s][b] + bias; y[b] = LN(x[b])  (the residual add fused with the next layer norm)
+hipError_t mz_dec_add_ln_launch(hipStream_t s, float* x, const float* parts, int nparts, long part_stride,
+                                const f16* bias, const f16* w, const f16* b, f16* y, int rows, int dim, float eps);
+// x[b] = emb[tok[b * maxT + p]] + pe[p] (fp32); y[b] = LN(x[b])
+hipError_t mz_dec_embed_ln_launch(hipStream_t s, const int* tok, const int* ctr, const f16* emb, const f16* pe,
+                                  float* x, const f16* w, const f16* b, f16* y, int rows, int dim, int maxT, float eps);
+// greedy choice of token p + 1 (kernels/whisper.cu:451-493 semantics) and, by the last block, ctr[0] += 1
+hipError_t mz_dec_argmax_launch(hipStream_t s, const float* logits, int V, const unsigned char* sup, int* tok, int* done,
+                                int* ctr, unsigned* counter, int B, int maxT, int prompt_len, int eos, int bs1, int bs2,
+                                int advance);

@@ -1,0 +1,107 @@
+"""The batch transcription API (src/transcribe.rs): prompts, then encode + greedy decode + token timestamps.
+
+The loop itself runs in the library (mz_transcribe, a C++ restatement of transcribe.rs:104-167: encoder groups,
+reset, optional language detection, one captured step graph replayed until every row is done, alignment rows to
+DTW). This module mirrors the Rust types around it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import dataclasses
+
+import numpy as np
+
+from . import _lib as L
+from ._lib import MzError, check, ptr
+from .model import NFRAMES, Engine, GenCfg
+
+
+class Prompt:
+    """start, language, task, no timestamps; English-only models: start, no timestamps (transcribe.rs:58-93)."""
+
+    def __init__(self, gc: GenCfg, language: str = "auto", task: str = "transcribe"):
+        self.multilingual = bool(gc.langs)
+        self.sot, self.no_timestamps = gc.sot, gc.no_timestamps
+        if not self.multilingual:
+            if language not in ("auto", "en") or task != "transcribe":
+                raise MzError("this English-only model takes only --language en (or auto) and --task transcribe")
+            self.task, self.lang = -1, None
+            return
+        if language == "auto":
+            self.lang = None
+        else:
+            self.lang = gc.lang_token(language)
+            if self.lang is None:
+                raise MzError(f"--language {language}: not a language of this model")
+        t = [tok for n, tok in gc.tasks if n == task]
+        if not t:
+            raise MzError(f"--task {task}: unknown task")
+        self.task = t[0]
+
+    def tokens(self, lang: int) -> list[int]:
+        return [self.sot, lang, self.task, self.no_timestamps] if self.multilingual else [self.sot, self.no_timestamps]
+
+    def detect(self) -> bool:
+        return self.multilingual and self.lang is None
+
+
+@dataclasses.dataclass
+class Decoded:
+    """One clip's result: language token, the whole sequence (prompt included) and each token's start time."""
+    lang: int
+    seq: list
+    ts: list
+
+
+@dataclasses.dataclass
+class Times:
+    enc: float = 0.0
+    dec: float = 0.0
+    post: float = 0.0
+    steps: int = 0
+
+
+def transcribe(e: Engine, mels: np.ndarray, p: Prompt, frames=None, graph: bool = True, max_new: int = 0,
+               half_align: bool = True) -> tuple[list[Decoded], Times]:
+    """Encode and decode up to e.bmax clips (log-mel f32 [n][n_mels][3000]); returns their tokens with timestamps.
+
+    max_new > 0 caps the generated tokens (the reference decodes until every row ends or max_t - 1 steps).
+    half_align rounds the timestamp arithmetic through fp16 where an fp16 model does (src/align.rs).
+    """
+    m = np.ascontiguousarray(mels, np.float32)
+    n = m.shape[0]
+    if m.shape[1:] != (e.dims.n_mels, NFRAMES):
+        raise MzError(f"mels must be [n][{e.dims.n_mels}][{NFRAMES}], got {m.shape}")
+    fr = np.ascontiguousarray(np.full(n, NFRAMES, np.int32) if frames is None else np.array(frames, np.int32))
+    prompt = np.array(p.tokens(p.lang if p.lang is not None else p.sot), np.int32)
+    mt = e.dims.max_t
+    seq = np.zeros((n, mt), np.int32)
+    seq_len = np.zeros(n, np.int32)
+    ts = np.zeros((n, mt), np.float32)
+    langs = np.zeros(n, np.int32)
+    tm = L.Times()
+    check(L.lib().mz_transcribe(e.h, ptr(m), ptr(fr), n, ptr(prompt), len(prompt), int(p.detect()), int(graph),
+                                int(max_new), int(half_align), ptr(seq), ptr(seq_len), ptr(ts), ptr(langs),
+                                C.byref(tm)))
+    out = [Decoded(int(langs[i]), seq[i, :seq_len[i]].tolist(), ts[i, :seq_len[i]].tolist()) for i in range(n)]
+    return out, Times(tm.enc, tm.dec, tm.post, tm.steps)
+
+
+def jump_times(w: np.ndarray, cols: int, width: int = 7, half: bool = True) -> np.ndarray:
+    """Token start times from alignment-head weights w [rows][heads][cols_full] (src/align.rs:8-63)."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, heads, full = w.shape
+    out = np.zeros(rows, np.float32)
+    check(L.lib().mz_jump_times(ptr(w), rows, heads, full, cols, width, int(half), ptr(out)))
+    return out
+
+
+def dtw(m: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """DTW path (text, time indices) over cost m [rows][cols] (src/align.rs:66-106)."""
+    m = np.ascontiguousarray(m, np.float64)
+    rows, cols = m.shape
+    text = np.zeros(rows + cols, np.int32)
+    time = np.zeros(rows + cols, np.int32)
+    n = np.zeros(1, np.int32)
+    check(L.lib().mz_dtw(ptr(m), rows, cols, ptr(text), ptr(time), ptr(n)))
+    return text[:n[0]], time[:n[0]]

@@ -1,0 +1,144 @@
+"""CPU checks of the C ABI: the library loads, exports every declared symbol, fails cleanly without a device, and its
+host helpers (fp16 conversion, DTW, token timestamps, config readers) match the reference's KATs and the oracle.
+No GPU work is launched here."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+from mimizuku_amd import _lib as L
+from mimizuku_amd import model, synth, transcribe
+from oracle import whisper_ref as R
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mimizuku.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mz_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    lib = L.lib()
+    names = declared_functions()
+    assert len(names) > 40
+    for n in names:
+        assert hasattr(lib, n), n
+    # and the Python binding declares a signature for each of them
+    assert set(names) == set(L.SIGNATURES), set(names) ^ set(L.SIGNATURES)
+
+
+def test_version_and_empty_error():
+    assert b"gfx950" in L.lib().mz_version()
+
+
+@pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="checks the no-device path")
+def test_init_without_device_is_a_clean_error():
+    with pytest.raises(L.MzError, match="device"):
+        model.Context()
+
+
+def test_fp16_conversion_exhaustive():
+    """src/gpu.rs:380-397: every binary16 pattern round-trips; RNE ties; overflow; subnormal ties."""
+    lib = L.lib()
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = h.view(np.float16).astype(np.float32)
+    for i in range(0, 65536, 1):
+        x = float(f[i])
+        y = lib.mz_h2f(int(h[i]))
+        if np.isnan(x):
+            assert np.isnan(y)
+            assert np.isnan(lib.mz_h2f(lib.mz_f2h(y)))
+        else:
+            assert y == x, hex(i)
+            assert lib.mz_f2h(y) == int(h[i]), hex(i)
+    assert lib.mz_f2h(1.0 + 1.0 / 2048.0) == 0x3C00
+    assert lib.mz_f2h(1.0 + 3.0 / 2048.0) == 0x3C02
+    assert lib.mz_f2h(65520.0) == 0x7C00
+    assert lib.mz_f2h(65519.0) == 0x7BFF
+    assert lib.mz_f2h(2.0 ** -25) == 0
+    assert lib.mz_f2h(3.0 * 2.0 ** -25) == 2
+    assert lib.mz_h2f(lib.mz_f2h(0.1)) == 1638.0 / 16384.0
+
+
+def test_fp16_conversion_matches_numpy_on_random_floats():
+    lib = L.lib()
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(3000) * s for s in (1e-6, 1e-3, 1, 1e3, 6e4)]).astype(np.float32)
+    want = x.astype(np.float16).view(np.uint16)
+    got = np.array([lib.mz_f2h(float(v)) for v in x], np.uint16)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_dtw_kat_and_oracle():
+    m = np.array([[-1.0 if (j // 2) == i else 1.0 for j in range(6)] for i in range(3)])
+    text, time = transcribe.dtw(m)
+    assert text.tolist() == [0, 0, 1, 1, 2, 2] and time.tolist() == [0, 1, 2, 3, 4, 5]
+    rng = np.random.default_rng(1)
+    for rows, cols in [(1, 1), (1, 9), (7, 3), (12, 40)]:
+        m = rng.standard_normal((rows, cols))
+        a, b = transcribe.dtw(m)
+        c, d = R.dtw(m)
+        np.testing.assert_array_equal(a, c)
+        np.testing.assert_array_equal(b, d)
+
+
+def test_jump_times_kat():
+    """src/align.rs:122-139"""
+    rows, full, cols = 4, 60, 40
+    w = np.zeros((rows, 1, full), np.float32)
+    for i in range(rows):
+        w[i, 0, 10 * i:10 * i + 10] = 0.1
+    for half in (True, False):
+        t = transcribe.jump_times(w, cols, 7, half)
+        assert np.all(np.abs(t - 0.2 * np.arange(rows)) < 0.03)
+        assert transcribe.jump_times(w, 0, 7, half).tolist() == [0.0] * rows
+        assert transcribe.jump_times(w[:1], cols, 7, half).tolist() == [0.0]
+
+
+@pytest.mark.parametrize("half", [False, True])
+def test_jump_times_match_oracle_on_softmax_weights(half):
+    rng = np.random.default_rng(2 + half)
+    for rows, heads, cols in [(5, 2, 30), (9, 6, 200), (3, 1, 2)]:
+        s = rng.standard_normal((rows, heads, 64)) * 3
+        w = np.exp(s - s.max(-1, keepdims=True))
+        w = (w / w.sum(-1, keepdims=True)).astype(np.float16).astype(np.float32)
+        np.testing.assert_array_equal(transcribe.jump_times(w, cols if cols <= 64 else 64, 7, half),
+                                      R.jump_times(w, cols if cols <= 64 else 64, 7, half))
+
+
+def test_jump_times_of_the_golden_weights():
+    fx = np.load(os.path.join(ROOT, "tests", "golden", "tiny_hfinit.npz"))
+    w = fx["align_w"][0].transpose(1, 0, 2)[4:]
+    np.testing.assert_array_equal(transcribe.jump_times(w, 1500, 7, half=False), fx["token_timestamps"][0][4:4 + len(w)])
+
+
+def test_config_readers(tmp_path):
+    g = synth.TINY
+    synth.write_model_dir(str(tmp_path), g, {"x": np.zeros(1, np.float16)})
+    d = model.Dims.load(str(tmp_path))
+    assert (d.d, d.nh, d.vocab, d.max_t) == (384, 6, 51865, 448)
+    gc = model.GenCfg.load(str(tmp_path), d)
+    assert gc.sot == 50258 and gc.eos == 50257 and gc.align_heads[0] == (2, 2)
+    assert gc.lang_token("ja") == 50266 and gc.lang_code(50259) == "en"
+    p = transcribe.Prompt(gc, "en", "transcribe")
+    assert p.tokens(p.lang) == [50258, 50259, 50359, 50363] and not p.detect()
+    assert transcribe.Prompt(gc).detect()
+    with pytest.raises(L.MzError):
+        transcribe.Prompt(gc, "xx")
+    bad = synth.generation_config(g)
+    bad["alignment_heads"] = [[9, 0]]
+    with pytest.raises(L.MzError):
+        model.GenCfg.from_dict(bad, d)
+
+
+def test_scratch_bytes_scales_with_batch():
+    d = model.Dims(1280, 5120, 20, 32, 32, 128, 51866, 448)
+    a = model.scratch_bytes(d, 10, 32, 8)
+    b = model.scratch_bytes(d, 10, 16, 8)
+    assert a > b > 0
+    # the cross k/v cache dominates the decoder's share: 32 rows x 32 layers x 2 x 20 heads x 1536 x 64 x 2 bytes
+    assert a - b >= 16 * 32 * 2 * 20 * 1536 * 64 * 2
