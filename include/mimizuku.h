@@ -75,7 +75,7 @@ int mz_gemm(mz_ctx* c, uint64_t x, int ldx, uint64_t w, uint64_t y, int ldy, int
 #define MZ_EPI_GELU_F16 1  /* out f16 [m][ldo] = gelu(acc + bias) (fc1; gelu_inplace fused, whisper.cu:106-113) */
 #define MZ_EPI_RESID_F32 2 /* out f32 [m][ldo] += acc + bias (residual add fused into out-proj / fc2) */
 #define MZ_EPI_GELU_POS 3  /* out f32 [m][ldo] = gelu(acc + bias) + pos[m % 1500][n] (conv2 + add_pos, whisper.cu:115-119) */
-#define MZ_EPI_HEADS 4     /* scatter into 1536 x 64 per-head tiles; v tiles transposed (see mz_linear_args) */
+#define MZ_EPI_HEADS 4     /* scatter into 1536 x 64 per-head tiles (see mz_linear_args) */
 
 /* One encoder-sized product on the tiled MFMA kernel (replaces fill_bias + cublasGemmStridedBatchedEx,
  * src/gpu.rs:229-235, and im2col1/im2col2, whisper.cu:121-139, when conv_cin > 0). */
@@ -91,7 +91,8 @@ typedef struct {
     uint64_t pos; /* MZ_EPI_GELU_POS: f16 [1500][n] */
     /* MZ_EPI_HEADS: column n -> block n / 64, row m -> clip m / 1500, time m % 1500; the block's tile is at
      * heads + ((slot0 + clip) * blocks_per_clip + block) * 1536 * 64 halves. kind 3: blocks [q|k|v][head] (encoder
-     * self-attention), kind 2: [layer][k|v][head] (cross-attention); v tiles are stored transposed [64][1536]. */
+     * self-attention; the v tiles stored transposed [64][1536]), kind 2: [layer][k|v][head] (cross-attention; every
+     * tile row-major [1536][64]). */
     uint64_t heads;
     int blocks_per_clip, nh, kind, slot0;
     /* implicit conv1d (kernel 3, padding 1): A[clip * conv_tout + t][tap * cin + ci] =
@@ -148,6 +149,8 @@ int mz_engine_finish(mz_engine* e);
 /* Encoder for n <= eg clips of log-mel f32 [n][n_mels][3000] (host); writes every decoder layer's cross k/v into
  * decoder slots slot0 .. slot0 + n - 1 (Engine::encode, src/model.rs:545-625). */
 int mz_engine_encode(mz_engine* e, const float* mels, int n, int slot0);
+/* As mz_engine_encode with the log-mel already in device memory (f32 [n][n_mels][3000] at `mels`): no host copy. */
+int mz_engine_encode_device(mz_engine* e, uint64_t mels, int n, int slot0);
 /* Prompt tokens [n][prompt_len] into rows 0..n-1, every row unfinished, position 0 (Engine::reset, :628-637). */
 int mz_engine_reset(mz_engine* e, const int32_t* prompts, int n, int prompt_len);
 /* One step on the start token restricted to language tokens; writes token 1 of each row and returns them in
@@ -162,6 +165,23 @@ int mz_engine_replay(mz_engine* e);
 /* Keep a copy of every encoder layer's input (fp32 residual stream) of the next encode (Engine::trace). */
 int mz_engine_set_trace(mz_engine* e, int on);
 
+/* Kernel timing (the reference's stage timings, src/main.rs:213-222, at kernel granularity): with profiling on, every
+ * encoder launch and every graph replay is bracketed by events on the engine's stream. mz_engine_profile clears the
+ * records; mz_engine_profile_read sums the elapsed time and counts the launches of one kernel class. */
+#define MZ_K_MEL 0   /* log-mel layout change */
+#define MZ_K_CONV1 1 /* conv1 + GELU (implicit GEMM) */
+#define MZ_K_CONV2 2 /* conv2 + GELU + positions */
+#define MZ_K_LN 3    /* encoder LayerNorm */
+#define MZ_K_QKV 4   /* fused q/k/v projection into per-head tiles */
+#define MZ_K_ATTN 5  /* encoder self-attention */
+#define MZ_K_OPROJ 6 /* out-projection + residual */
+#define MZ_K_FC1 7   /* fc1 + GELU */
+#define MZ_K_FC2 8   /* fc2 + residual */
+#define MZ_K_XKV 9   /* every decoder layer's cross k/v */
+#define MZ_K_STEP 10 /* one replay of the captured decoder step */
+int mz_engine_profile(mz_engine* e, int on);
+int mz_engine_profile_read(mz_engine* e, int kernel, double* total_ms, int* count);
+
 #define MZ_BUF_TOK 0     /* i32 [bmax][max_t] */
 #define MZ_BUF_DONE 1    /* i32 [bmax] */
 #define MZ_BUF_CTR 2     /* i32 [4]; ctr[0] = position of the next step */
@@ -169,7 +189,7 @@ int mz_engine_set_trace(mz_engine* e, int on);
 #define MZ_BUF_ENC_OUT 4 /* f16 [eg * 1500][d] final-LN encoder output of the last encode */
 #define MZ_BUF_LOGITS 5  /* f32 [bmax][vocab] logits of the last step */
 #define MZ_BUF_TRACE 6   /* f32 [enc_layers][eg * 1500][d] encoder layer inputs (set_trace) */
-#define MZ_BUF_XKV 7     /* f16 [bmax][dec_layers][2][nh] tiles of 1536 x 64 (k as [t][64], v transposed) */
+#define MZ_BUF_XKV 7     /* f16 [bmax][dec_layers][2][nh] tiles of 1536 x 64 (k, v as [t][64]) */
 #define MZ_BUF_DEC_X 8   /* f32 [bmax][d] decoder residual stream */
 #define MZ_BUF_ENC_X 9   /* f32 [eg * 1500][d] encoder residual stream */
 /* Device address and size of an engine buffer. */
@@ -193,6 +213,10 @@ typedef struct {
 int mz_transcribe(mz_engine* e, const float* mels, const int32_t* frames, int n, const int32_t* prompt,
                   int prompt_len, int detect, int use_graph, int max_new, int half_align, int32_t* seq,
                   int32_t* seq_len, float* ts, int32_t* langs, mz_times* times);
+/* As mz_transcribe with the log-mel already in device memory (f32 [n][n_mels][3000] at `mels`). */
+int mz_transcribe_device(mz_engine* e, uint64_t mels, const int32_t* frames, int n, const int32_t* prompt,
+                         int prompt_len, int detect, int use_graph, int max_new, int half_align, int32_t* seq,
+                         int32_t* seq_len, float* ts, int32_t* langs, mz_times* times);
 
 /* ------------------------------------------------------------------ host helpers */
 

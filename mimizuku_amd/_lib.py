@@ -44,6 +44,8 @@ class Times(C.Structure):
 EPI_F16, EPI_GELU_F16, EPI_RESID_F32, EPI_GELU_POS, EPI_HEADS = range(5)
 BUF_TOK, BUF_DONE, BUF_CTR, BUF_ALIGN, BUF_ENC_OUT, BUF_LOGITS, BUF_TRACE, BUF_XKV, BUF_DEC_X, BUF_ENC_X = range(10)
 DT_F16, DT_F32 = 0, 1
+# kernel classes of mz_engine_profile_read
+K_NAMES = ["mel", "conv1", "conv2", "ln", "qkv", "attn", "oproj", "fc1", "fc2", "xkv", "step"]
 
 # name -> (restype, argtypes); every int-returning function is a status
 SIGNATURES = {
@@ -77,6 +79,9 @@ SIGNATURES = {
     "mz_engine_put": (i32, [P, C.c_char_p, i32, P, C.POINTER(C.c_int64), i32]),
     "mz_engine_finish": (i32, [P]),
     "mz_engine_encode": (i32, [P, P, i32, i32]),
+    "mz_engine_encode_device": (i32, [P, u64, i32, i32]),
+    "mz_engine_profile": (i32, [P, i32]),
+    "mz_engine_profile_read": (i32, [P, i32, C.POINTER(C.c_double), C.POINTER(i32)]),
     "mz_engine_reset": (i32, [P, P, i32, i32]),
     "mz_engine_detect": (i32, [P, i32, P]),
     "mz_engine_step": (i32, [P, i32, i32, i32]),
@@ -87,6 +92,7 @@ SIGNATURES = {
     "mz_engine_read": (i32, [P, i32, P, sz, sz]),
     "mz_engine_free": (i32, [P]),
     "mz_transcribe": (i32, [P, P, P, i32, P, i32, i32, i32, i32, i32, P, P, P, P, C.POINTER(Times)]),
+    "mz_transcribe_device": (i32, [P, u64, P, i32, P, i32, i32, i32, i32, i32, P, P, P, P, C.POINTER(Times)]),
     "mz_jump_times": (i32, [P, i32, i32, i32, i32, i32, i32, P]),
     "mz_dtw": (i32, [P, i32, i32, P, P, P]),
     "mz_f2h": (C.c_uint16, [f32]),

@@ -1,5 +1,7 @@
 // Host-side helpers: IEEE binary16 conversions and the token-timestamp alignment (median filter + DTW over the
 // alignment heads' cross-attention), following src/align.rs:8-106 and transformers' _extract_token_timestamps.
+#include <immintrin.h>
+
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -50,16 +52,21 @@ extern "C" float mz_h2f(uint16_t h) { return mz_h2f_host(h); }
 
 static inline float rh(float x) { return mz_h2f_host(mz_f2h_host(x)); }
 
-// DTW over cost m [rows][cols] with a float32 cost table; ties go to the horizontal move (j - 1).
+// DTW over cost m [rows][cols] with a float32 cost table; ties go to the horizontal move (j - 1). Cells are filled
+// row by row: each depends only on its left, upper and upper-left neighbours, so the table equals the column-order
+// fill of the numpy reference while walking memory contiguously.
 static void dtw_path(const double* m, int rows, int cols, std::vector<int>& text, std::vector<int>& time) {
     const int w = cols + 1;
     std::vector<float> cost((size_t)(rows + 1) * w, INFINITY);
     std::vector<int8_t> trace((size_t)(rows + 1) * w, -1);
     cost[0] = 0.f;
-    for (int j = 1; j <= cols; j++)
-        for (int i = 1; i <= rows; i++) {
-            const float c0 = cost[(size_t)(i - 1) * w + j - 1], c1 = cost[(size_t)(i - 1) * w + j],
-                        c2 = cost[(size_t)i * w + j - 1];
+    for (int i = 1; i <= rows; i++) {
+        const float* up = &cost[(size_t)(i - 1) * w];
+        float* cur = &cost[(size_t)i * w];
+        int8_t* tr = &trace[(size_t)i * w];
+        const double* mr = m + (size_t)(i - 1) * cols;
+        for (int j = 1; j <= cols; j++) {
+            const float c0 = up[j - 1], c1 = up[j], c2 = cur[j - 1];
             float c;
             int8_t t;
             if (c0 < c1 && c0 < c2) {
@@ -72,9 +79,10 @@ static void dtw_path(const double* m, int rows, int cols, std::vector<int>& text
                 c = c2;
                 t = 2;
             }
-            cost[(size_t)i * w + j] = (float)(m[(size_t)(i - 1) * cols + j - 1] + (double)c);
-            trace[(size_t)i * w + j] = t;
+            cur[j] = (float)(mr[j - 1] + (double)c);
+            tr[j] = t;
         }
+    }
     for (int j = 0; j <= cols; j++) trace[j] = 2;
     for (int i = 0; i <= rows; i++) trace[(size_t)i * w] = 1;
     text.clear();
@@ -109,65 +117,107 @@ extern "C" int mz_dtw(const double* m, int rows, int cols, int32_t* text, int32_
     return MZ_OK;
 }
 
-extern "C" int mz_jump_times(const float* w, int rows, int heads, int cols_full, int cols, int width, int half,
-                             float* out) {
-    if (!w || !out || rows < 0 || heads <= 0 || cols < 0 || cols > cols_full || width <= 0 || width % 2 == 0)
-        return mz_fail(MZ_ERR_ARG, "mz_jump_times: bad argument");
-    if (rows == 0) return MZ_OK;
+namespace {
+
+// This file is built with F16C and AVX2 (checked at run time by host_ok): the fp16 round trips of the timestamp
+// arithmetic use the hardware conversion (round to nearest even, as the software mz_f2h_host), and the median
+// network vectorises over frames.
+inline float rhw(float x) { return _cvtsh_ss(_cvtss_sh(x, 0)); }
+inline float load_w(const float* w, size_t i) { return w[i]; }
+inline float load_w(const uint16_t* w, size_t i) { return _cvtsh_ss(w[i]); }
+
+inline void cswap(float& a, float& b) {
+    const float lo = a < b ? a : b, hi = a < b ? b : a;
+    a = lo;
+    b = hi;
+}
+
+// median of 7 finite values: a 16-comparator sorting network, middle element
+inline float median7(const float* p) {
+    float a[7] = {p[0], p[1], p[2], p[3], p[4], p[5], p[6]};
+    cswap(a[0], a[6]), cswap(a[2], a[3]), cswap(a[4], a[5]);
+    cswap(a[0], a[2]), cswap(a[1], a[4]), cswap(a[3], a[6]);
+    cswap(a[0], a[1]), cswap(a[2], a[5]), cswap(a[3], a[4]);
+    cswap(a[1], a[2]), cswap(a[4], a[6]);
+    cswap(a[2], a[3]), cswap(a[4], a[5]);
+    cswap(a[1], a[2]), cswap(a[3], a[4]), cswap(a[5], a[6]);
+    return a[3];
+}
+
+// Token start times (src/align.rs:8-63) from w [rows][heads][cols_full] (f32 or fp16 bits).
+template <class T>
+void jump_times_impl(const T* w, int rows, int heads, int cols_full, int cols, int width, int half, float* out) {
+    if (rows == 0) return;
     if (cols == 0) {
         std::fill(out, out + rows, 0.f);
-        return MZ_OK;
+        return;
     }
-    auto at = [&](int i, int a, int j) { return w[((size_t)i * heads + a) * cols_full + j]; };
     const int pad = width / 2;
-    std::vector<float> avg((size_t)rows * cols, 0.f), z((size_t)rows * cols), win(width);
+    std::vector<float> avg((size_t)rows * cols, 0.f), z((size_t)rows * cols), win(width), padded(cols + 2 * pad);
+    std::vector<double> sum(cols), sq(cols);
+    std::vector<float> mean(cols), sd(cols);
     for (int a = 0; a < heads; a++) {
         // normalise each column over the rows (population std); a constant column scores 0
+        std::fill(sum.begin(), sum.end(), 0.0);
+        std::fill(sq.begin(), sq.end(), 0.0);
+        for (int i = 0; i < rows; i++) {
+            const size_t o = ((size_t)i * heads + a) * cols_full;
+            for (int j = 0; j < cols; j++) sum[j] += load_w(w, o + j);
+        }
+        for (int j = 0; j < cols; j++) mean[j] = (float)(sum[j] / rows);
+        for (int i = 0; i < rows; i++) {
+            const size_t o = ((size_t)i * heads + a) * cols_full;
+            for (int j = 0; j < cols; j++) {
+                const double dv = (double)(load_w(w, o + j) - mean[j]);
+                sq[j] += dv * dv;
+            }
+        }
         for (int j = 0; j < cols; j++) {
-            double s = 0;
-            for (int i = 0; i < rows; i++) s += at(i, a, j);
-            float mean = (float)(s / rows);
-            double q = 0;
-            for (int i = 0; i < rows; i++) {
-                const double dv = (double)(at(i, a, j) - mean);
-                q += dv * dv;
-            }
-            float sd = std::sqrt((float)(q / rows));
+            sd[j] = std::sqrt((float)(sq[j] / rows));
             if (half) {
-                mean = rh(mean);
-                sd = rh(sd);
+                mean[j] = rhw(mean[j]);
+                sd[j] = rhw(sd[j]);
             }
-            for (int i = 0; i < rows; i++) {
+        }
+        for (int i = 0; i < rows; i++) {
+            const size_t o = ((size_t)i * heads + a) * cols_full;
+            float* zr = &z[(size_t)i * cols];
+            for (int j = 0; j < cols; j++) {
+                const float x = load_w(w, o + j);
                 float v = 0.f;
-                if (sd > 0.f) v = half ? rh(rh(at(i, a, j) - mean) / sd) : (at(i, a, j) - mean) / sd;
-                z[(size_t)i * cols + j] = v;
+                if (sd[j] > 0.f) v = half ? rhw(rhw(x - mean[j]) / sd[j]) : (x - mean[j]) / sd[j];
+                zr[j] = v;
             }
         }
         // median over a width-`width` window with reflect padding, then accumulate over heads
         for (int i = 0; i < rows; i++) {
             const float* row = &z[(size_t)i * cols];
-            for (int j = 0; j < cols; j++) {
-                float v;
-                if (cols <= pad) {
-                    v = row[j];
-                } else {
-                    for (int k = 0; k < width; k++) {
-                        int t = j + k - pad;
-                        if (t < 0) t = -t;
-                        if (t >= cols) t = 2 * (cols - 1) - t;
-                        win[k] = row[t];
-                    }
+            float* ar = &avg[(size_t)i * cols];
+            if (cols <= pad) {
+                for (int j = 0; j < cols; j++) ar[j] += row[j];
+                continue;
+            }
+            for (int k = 0; k < cols + 2 * pad; k++) {
+                int t = k - pad;
+                if (t < 0) t = -t;
+                if (t >= cols) t = 2 * (cols - 1) - t;
+                padded[k] = row[t];
+            }
+            if (width == 7) {
+                for (int j = 0; j < cols; j++) ar[j] += median7(&padded[j]);
+            } else {
+                for (int j = 0; j < cols; j++) {
+                    std::copy(&padded[j], &padded[j] + width, win.begin());
                     std::nth_element(win.begin(), win.begin() + pad, win.end());
-                    v = win[pad];
+                    ar[j] += win[pad];
                 }
-                avg[(size_t)i * cols + j] += v;
             }
         }
     }
     std::vector<double> m((size_t)rows * cols);
     for (size_t k = 0; k < m.size(); k++) {
         float s = avg[k] / (float)heads;
-        if (half) s = rh(s);
+        if (half) s = rhw(s);
         m[k] = -(double)s;
     }
     std::vector<int> text, time;
@@ -177,5 +227,33 @@ extern "C" int mz_jump_times(const float* w, int rows, int heads, int cols_full,
         if (k == 0 || text[k] != text[k - 1]) out[n++] = (float)((double)time[k] * 0.02);
     const float lastv = n ? out[n - 1] : 0.f;
     for (; n < rows; n++) out[n] = lastv;  // degenerate scores can bend the path (src/align.rs:60-61)
+}
+
+}  // namespace
+
+static bool jump_args_ok(int rows, int heads, int cols_full, int cols, int width) {
+    return rows >= 0 && heads > 0 && cols >= 0 && cols <= cols_full && width > 0 && width % 2 == 1;
+}
+
+static int host_ok() {
+    static const bool ok = __builtin_cpu_supports("f16c") && __builtin_cpu_supports("avx2");
+    return ok ? MZ_OK : mz_fail(MZ_ERR_STATE, "token timestamps need a host CPU with F16C and AVX2");
+}
+
+extern "C" int mz_jump_times(const float* w, int rows, int heads, int cols_full, int cols, int width, int half,
+                             float* out) {
+    if (!w || !out || !jump_args_ok(rows, heads, cols_full, cols, width))
+        return mz_fail(MZ_ERR_ARG, "mz_jump_times: bad argument");
+    if (int r = host_ok()) return r;
+    jump_times_impl(w, rows, heads, cols_full, cols, width, half, out);
+    return MZ_OK;
+}
+
+int mz_jump_times_f16(const uint16_t* w, int rows, int heads, int cols_full, int cols, int width, int half,
+                      float* out) {
+    if (!w || !out || !jump_args_ok(rows, heads, cols_full, cols, width))
+        return mz_fail(MZ_ERR_ARG, "mz_jump_times: bad argument");
+    if (int r = host_ok()) return r;
+    jump_times_impl(w, rows, heads, cols_full, cols, width, half, out);
     return MZ_OK;
 }

@@ -11,7 +11,9 @@
 #include <cstring>
 #include <map>
 #include <set>
+#include <atomic>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/mimizuku.h"
@@ -22,7 +24,6 @@ namespace {
 
 constexpr int HD = 64, TENC = 1500, TPAD = 1536, NFR = 3000;
 constexpr float EPS = 1e-5f;
-constexpr int XCHUNK = 384;  // cross-attention keys per block (4 blocks per row and head)
 
 struct Ln {
     f16 *w = nullptr, *b = nullptr;
@@ -82,14 +83,37 @@ struct mz_engine {
     f16* xkvbuf = nullptr;
     int *tok = nullptr, *done = nullptr, *ctr = nullptr;
     float *x = nullptr, *q = nullptr, *part = nullptr, *logits = nullptr;
-    f16 *h = nullptr, *datt = nullptr, *dff = nullptr, *kc = nullptr, *vct = nullptr, *align = nullptr;
-    float *xpart = nullptr, *sal = nullptr;
-    unsigned *xcnt = nullptr, *acnt = nullptr;
+    f16 *h = nullptr, *datt = nullptr, *dff = nullptr, *kc = nullptr, *vc = nullptr, *align = nullptr;
+    int2* amax = nullptr;  // LM head argmax partials [ceil(vocab / 32)][bmax]
     int* aslot = nullptr;
     unsigned char *sup = nullptr, *sup_lang = nullptr;
     size_t part_elems = 0;
     mz_graph* graph = nullptr;
     int graph_b = -1, graph_np = -1;
+    // kernel timing (mz_engine_profile): events around each encoder launch and each decoder step
+    bool prof_on = false;
+    struct Rec {
+        int id;
+        hipEvent_t a, b;
+    };
+    std::vector<Rec> recs;
+    std::vector<hipEvent_t> evpool;
+    hipEvent_t ev() {
+        if (!evpool.empty()) {
+            hipEvent_t x = evpool.back();
+            evpool.pop_back();
+            return x;
+        }
+        hipEvent_t x = nullptr;
+        if (hipEventCreate(&x) != hipSuccess) return nullptr;
+        return x;
+    }
+    // pinned host staging of the alignment rows read back after decoding (hipHostMalloc'd on first use)
+    uint16_t* align_host = nullptr;
+    size_t align_host_bytes = 0;
+    // position of the next step as the host has enqueued it (the device copy is ctr[0]); steps beyond the cache
+    // (max_t - 1 of them after a reset) are refused
+    int host_pos = 0;
 
     template <class T>
     int alloc(T** p, size_t n) {
@@ -121,14 +145,14 @@ size_t weight_elems(const mz_dims& d, int* k1pad) {
 }
 
 int ksplit_for(int N, int K) {
-    // split K until the grid has a few hundred blocks, keeping >= 4 groups of 64 per block (one per wave)
+    // Split K over workgroups until the grid covers the 256 CUs, keeping at most 4 groups of 64 columns per wave
+    // (one batch of loads in flight) and at most MZ_MAX_PARTS partials.
     const int tiles = (N + 31) / 32, groups = K / 64;
     int best = 1;
-    for (int ks = 1; ks <= groups; ks++) {
-        if (groups % ks || groups / ks < 4) continue;
-        if ((long)tiles * ks > 1024) break;
+    for (int ks = 1; ks <= std::min(groups, MZ_MAX_PARTS); ks++) {
+        if (groups % ks) continue;
         best = ks;
-        if ((long)tiles * ks >= 256) break;
+        if (groups / ks <= 16 && (long)tiles * ks >= 192) break;
     }
     return best;
 }
@@ -142,9 +166,9 @@ extern "C" size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int 
     size_t enc = G * d->n_mels * NFR * 4 + G * NFR * d->n_mels * 2 + G * NFR * D * 2 + G * TENC * D * 4 +
                  G * TENC * D * 2 * 2 + G * 3 * nh * TPAD * HD * 2 + G * TENC * F * 2;
     size_t dec = B * nl * 2 * nh * TPAD * HD * 2 + B * mt * 4 + B * 4 + 16 + B * D * 4 * 2 + B * D * 2 * 2 + B * F * 2 +
-                 2 * nl * B * nh * mt * HD * 2 + B * V * 4 + B * mt * n_align * TENC * 2 + B * nh * 4 * 66 * 4 +
-                 B * nh * 4 + B * n_align * TPAD * 4 + nl * nh * 4 + 2 * V;
-    size_t part = 20 * B * D * 4 + 4 * B * F * 4;
+                 2 * nl * B * nh * mt * HD * 2 + B * V * 4 + B * mt * n_align * TENC * 2 + (V + 31) / 32 * B * 8 +
+                 nl * nh * 4 + 2 * V;
+    size_t part = (size_t)MZ_MAX_PARTS * B * D * 4;
     return enc + dec + part;
 }
 
@@ -284,10 +308,9 @@ extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, in
         (r = e->alloc(&e->done, B)) || (r = e->alloc(&e->ctr, 4)) || (r = e->alloc(&e->x, B * D)) ||
         (r = e->alloc(&e->q, B * D)) || (r = e->alloc(&e->h, B * D)) || (r = e->alloc(&e->datt, B * D)) ||
         (r = e->alloc(&e->dff, B * F)) || (r = e->alloc(&e->kc, (size_t)nl * B * nh * mt * HD)) ||
-        (r = e->alloc(&e->vct, (size_t)nl * B * nh * HD * mt)) || (r = e->alloc(&e->logits, B * V)) ||
+        (r = e->alloc(&e->vc, (size_t)nl * B * nh * mt * HD)) || (r = e->alloc(&e->logits, B * V)) ||
         (r = e->alloc(&e->align, B * mt * e->na * (size_t)TENC)) ||
-        (r = e->alloc(&e->xpart, B * nh * ((TENC + XCHUNK - 1) / XCHUNK) * 66)) || (r = e->alloc(&e->xcnt, B * nh)) ||
-        (r = e->alloc(&e->acnt, 4)) || (r = e->alloc(&e->sal, B * e->na * (size_t)TPAD)) ||
+        (r = e->alloc(&e->amax, (size_t)((V + 31) / 32) * B)) ||
         (r = e->alloc(&e->aslot, (size_t)nl * nh)) || (r = e->alloc(&e->sup, V)) || (r = e->alloc(&e->sup_lang, V)))
         return fail(r);
     // split-K partials: the largest ks * rows * n over the decoder products
@@ -375,7 +398,24 @@ extern "C" int mz_engine_set_trace(mz_engine* e, int on) {
         if (int _r = mz_hip((expr), what)) return _r;       \
     } while (0)
 
-extern "C" int mz_engine_encode(mz_engine* e, const float* mels, int n, int slot0) {
+// Times `expr` (one kernel launch) with a pair of events when profiling is on.
+#define PROF(id, expr, what)                                                        \
+    do {                                                                            \
+        hipEvent_t _a = nullptr, _b = nullptr;                                      \
+        if (e->prof_on) {                                                           \
+            _a = e->ev();                                                           \
+            _b = e->ev();                                                           \
+            if (!_a || !_b) return mz_fail(MZ_ERR_HIP, "hipEventCreate failed");     \
+            TRY(hipEventRecord(_a, s), "hipEventRecord");                          \
+        }                                                                           \
+        TRY((expr), what);                                                          \
+        if (e->prof_on) {                                                           \
+            TRY(hipEventRecord(_b, s), "hipEventRecord");                          \
+            e->recs.push_back({(id), _a, _b});                                      \
+        }                                                                           \
+    } while (0)
+
+static int encode_impl(mz_engine* e, const float* mels, bool on_device, int n, int slot0) {
     if (!e || !mels) return mz_fail(MZ_ERR_ARG, "mz_engine_encode: null argument");
     if (!e->loaded) return mz_fail(MZ_ERR_STATE, "mz_engine_encode: weights not loaded (mz_engine_finish)");
     if (n <= 0 || n > e->eg || slot0 < 0 || slot0 + n > e->bmax)
@@ -383,8 +423,12 @@ extern "C" int mz_engine_encode(mz_engine* e, const float* mels, int n, int slot
     hipStream_t s = e->c->stream;
     const int D = e->dm.d, nm = e->dm.n_mels, nh = e->dm.nh, F = e->dm.ff, nl = e->dm.dec_layers;
     const int rows = n * TENC;
-    TRY(hipMemcpyAsync(e->mel, mels, (size_t)n * nm * NFR * 4, hipMemcpyHostToDevice, s), "mel upload");
-    TRY(mz_mel_transpose_launch(s, e->mel, e->melT, n, nm), "mel transpose");
+    const float* src = mels;
+    if (!on_device) {
+        TRY(hipMemcpyAsync(e->mel, mels, (size_t)n * nm * NFR * 4, hipMemcpyHostToDevice, s), "mel upload");
+        src = e->mel;
+    }
+    PROF(MZ_K_MEL, mz_mel_transpose_launch(s, src, e->melT, n, nm), "mel transpose");
     // conv stem as implicit GEMMs (src/model.rs:552-558): GELU(conv1), GELU(conv2, stride 2) + positions
     MzGemm g{};
     g.A = e->melT;
@@ -399,7 +443,7 @@ extern "C" int mz_engine_encode(mz_engine* e, const float* mels, int n, int slot
     g.conv_stride = 1;
     g.out = e->h1;
     g.ldo = D;
-    TRY(mz_gemm_launch(s, ALOAD_CONV, EPI_GELU_F16, g), "conv1");
+    PROF(MZ_K_CONV1, mz_gemm_launch(s, ALOAD_CONV, EPI_GELU_F16, g), "conv1");
     g = MzGemm{};
     g.A = e->h1;
     g.W = e->conv2.w;
@@ -414,8 +458,8 @@ extern "C" int mz_engine_encode(mz_engine* e, const float* mels, int n, int slot
     g.out = e->ex;
     g.ldo = D;
     g.pos = e->epos;
-    TRY(mz_gemm_launch(s, ALOAD_CONV, EPI_GELU_POS, g), "conv2");
-    TRY(mz_layernorm_launch(s, e->ex, D, e->encv[0].ln1.w, e->encv[0].ln1.b, e->hb, D, rows, D, EPS), "ln");
+    PROF(MZ_K_CONV2, mz_gemm_launch(s, ALOAD_CONV, EPI_GELU_POS, g), "conv2");
+    PROF(MZ_K_LN, mz_layernorm_launch(s, e->ex, D, e->encv[0].ln1.w, e->encv[0].ln1.b, e->hb, D, rows, D, EPS), "ln");
     for (int i = 0; i < e->dm.enc_layers; i++) {
         const EncLayer& L = e->encv[i];
         if (e->trace_on)
@@ -434,8 +478,8 @@ extern "C" int mz_engine_encode(mz_engine* e, const float* mels, int n, int slot
         g.blocks_per_clip = 3 * nh;
         g.nh = nh;
         g.kind = 3;
-        TRY(mz_gemm_launch(s, ALOAD_PLAIN, EPI_HEADS, g), "qkv");
-        TRY(mz_enc_attention_launch(s, e->qkvh, e->att, n, nh), "attention");
+        PROF(MZ_K_QKV, mz_gemm_launch(s, ALOAD_PLAIN, EPI_HEADS, g), "qkv");
+        PROF(MZ_K_ATTN, mz_enc_attention_launch(s, e->qkvh, e->att, n, nh), "attention");
         g = MzGemm{};
         g.A = e->att;
         g.lda = D;
@@ -446,15 +490,15 @@ extern "C" int mz_engine_encode(mz_engine* e, const float* mels, int n, int slot
         g.K = D;
         g.out = e->ex;
         g.ldo = D;
-        TRY(mz_gemm_launch(s, ALOAD_PLAIN, EPI_RESID_F32, g), "out-proj");
-        TRY(mz_layernorm_launch(s, e->ex, D, L.ln2.w, L.ln2.b, e->hb, D, rows, D, EPS), "ln2");
+        PROF(MZ_K_OPROJ, mz_gemm_launch(s, ALOAD_PLAIN, EPI_RESID_F32, g), "out-proj");
+        PROF(MZ_K_LN, mz_layernorm_launch(s, e->ex, D, L.ln2.w, L.ln2.b, e->hb, D, rows, D, EPS), "ln2");
         g.A = e->hb;
         g.W = L.fc1.w;
         g.bias = L.fc1.b;
         g.N = F;
         g.out = e->ff;
         g.ldo = F;
-        TRY(mz_gemm_launch(s, ALOAD_PLAIN, EPI_GELU_F16, g), "fc1");
+        PROF(MZ_K_FC1, mz_gemm_launch(s, ALOAD_PLAIN, EPI_GELU_F16, g), "fc1");
         g.A = e->ff;
         g.lda = F;
         g.W = L.fc2.w;
@@ -463,9 +507,9 @@ extern "C" int mz_engine_encode(mz_engine* e, const float* mels, int n, int slot
         g.K = F;
         g.out = e->ex;
         g.ldo = D;
-        TRY(mz_gemm_launch(s, ALOAD_PLAIN, EPI_RESID_F32, g), "fc2");
+        PROF(MZ_K_FC2, mz_gemm_launch(s, ALOAD_PLAIN, EPI_RESID_F32, g), "fc2");
         const Ln& nx = i + 1 < e->dm.enc_layers ? e->encv[i + 1].ln1 : e->eln;  // the last one is the final LN
-        TRY(mz_layernorm_launch(s, e->ex, D, nx.w, nx.b, e->hb, D, rows, D, EPS), "ln");
+        PROF(MZ_K_LN, mz_layernorm_launch(s, e->ex, D, nx.w, nx.b, e->hb, D, rows, D, EPS), "ln");
     }
     // cross k/v of every decoder layer for the clips' slots (src/model.rs:614-623)
     g = MzGemm{};
@@ -481,7 +525,44 @@ extern "C" int mz_engine_encode(mz_engine* e, const float* mels, int n, int slot
     g.nh = nh;
     g.kind = 2;
     g.slot0 = slot0;
-    TRY(mz_gemm_launch(s, ALOAD_PLAIN, EPI_HEADS, g), "cross k/v");
+    PROF(MZ_K_XKV, mz_gemm_launch(s, ALOAD_PLAIN, EPI_HEADS, g), "cross k/v");
+    return MZ_OK;
+}
+
+extern "C" int mz_engine_encode(mz_engine* e, const float* mels, int n, int slot0) {
+    return encode_impl(e, mels, false, n, slot0);
+}
+
+extern "C" int mz_engine_encode_device(mz_engine* e, uint64_t mels, int n, int slot0) {
+    return encode_impl(e, (const float*)(uintptr_t)mels, true, n, slot0);
+}
+
+extern "C" int mz_engine_profile(mz_engine* e, int on) {
+    if (!e) return mz_fail(MZ_ERR_ARG, "mz_engine_profile: null engine");
+    if (int r = mz_sync(e->c)) return r;
+    for (auto& r : e->recs) {
+        e->evpool.push_back(r.a);
+        e->evpool.push_back(r.b);
+    }
+    e->recs.clear();
+    e->prof_on = on != 0;
+    return MZ_OK;
+}
+
+extern "C" int mz_engine_profile_read(mz_engine* e, int id, double* total_ms, int* count) {
+    if (!e || !total_ms || !count) return mz_fail(MZ_ERR_ARG, "mz_engine_profile_read: null argument");
+    if (int r = mz_sync(e->c)) return r;
+    double t = 0;
+    int n = 0;
+    for (auto& r : e->recs)
+        if (r.id == id) {
+            float ms = 0;
+            if (int rc = mz_hip(hipEventElapsedTime(&ms, r.a, r.b), "hipEventElapsedTime")) return rc;
+            t += ms;
+            n++;
+        }
+    *total_ms = t;
+    *count = n;
     return MZ_OK;
 }
 
@@ -500,7 +581,17 @@ extern "C" int mz_engine_reset(mz_engine* e, const int32_t* prompts, int n, int 
     std::vector<int32_t> zeros(std::max(n, 4), 0);
     if (int r = mz_upload(e->c, (uint64_t)(uintptr_t)e->tok, t.data(), t.size() * 4)) return r;
     if (int r = mz_upload(e->c, (uint64_t)(uintptr_t)e->done, zeros.data(), (size_t)n * 4)) return r;
-    return mz_upload(e->c, (uint64_t)(uintptr_t)e->ctr, zeros.data(), 16);
+    if (int r = mz_upload(e->c, (uint64_t)(uintptr_t)e->ctr, zeros.data(), 16)) return r;
+    e->host_pos = 0;
+    return MZ_OK;
+}
+
+static int take_position(mz_engine* e) {
+    if (e->host_pos >= e->dm.max_t - 1)
+        return mz_fail(MZ_ERR_STATE, "decoder position %d: the cache holds %d positions (reset first)", e->host_pos,
+                       e->dm.max_t);
+    e->host_pos++;
+    return MZ_OK;
 }
 
 static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
@@ -522,13 +613,38 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
         g.ksplit = ks;
         g.out = out;
         g.ldo = ldo;
+        g.ctr = e->ctr;
         return mz_dec_gemm_launch(s, epi, g);
+    };
+    auto attn = [&](const float* q, int nq, const f16* qbias, const f16* k, const f16* v, long kv_b, int L,
+                    const int* aslot) {
+        MzDecAttn a{};
+        a.q = q;
+        a.nq = nq;
+        a.qstride = (long)b * D;
+        a.qbias = qbias;
+        a.k = k;
+        a.v = v;
+        a.kv_b = kv_b;
+        a.kv_h = L > 0 ? blk : (long)mt * HD;
+        a.L = L;
+        a.ctr = e->ctr;
+        a.done = e->done;
+        a.out = e->datt;
+        a.B = b;
+        a.nh = nh;
+        a.d = D;
+        a.maxT = mt;
+        a.aslot = aslot;
+        a.align = e->align;
+        a.na = e->na;
+        return mz_dec_attn_launch(s, a);
     };
     const int ks_dd = ksplit_for(D, D), ks_df = ksplit_for(D, F);
     for (int i = 0; i < nl; i++) {
         const DecLayer& L = e->decv[i];
         f16* kc = e->kc + (size_t)i * e->bmax * nh * mt * HD;
-        f16* vct = e->vct + (size_t)i * e->bmax * nh * HD * mt;
+        f16* vc = e->vc + (size_t)i * e->bmax * nh * mt * HD;
         {
             MzDec g{};
             g.x = e->h;
@@ -542,60 +658,19 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
             g.out = e->q;
             g.ldo = D;
             g.kc = kc;
-            g.vct = vct;
+            g.vc = vc;
             g.ctr = e->ctr;
             g.maxT = mt;
             g.d = D;
             TRY(mz_dec_gemm_launch(s, DEPI_QKV, g), "dec qkv");
         }
-        MzDecAttn a{};
-        a.q = e->q;
-        a.nq = 1;
-        a.k = kc;
-        a.vt = vct;
-        a.kv_b = (long)nh * mt * HD;
-        a.kv_h = (long)mt * HD;
-        a.vt_ld = mt;
-        a.L = -1;
-        a.ctr = e->ctr;
-        a.done = e->done;
-        a.out = e->datt;
-        a.B = b;
-        a.nh = nh;
-        a.d = D;
-        a.nsplit = 1;
-        a.chunk = rup(mt, 8);
-        TRY(mz_dec_attn_launch(s, a), "self attention");
+        TRY(attn(e->q, 1, nullptr, kc, vc, (long)nh * mt * HD, -1, nullptr), "self attention");
         TRY(gemm(DEPI_PARTIAL, e->datt, D, L.o, D, D, ks_dd, e->part, D), "dec out-proj");
         TRY(mz_dec_add_ln_launch(s, e->x, e->part, ks_dd, (long)b * D, L.o.b, L.lnx.w, L.lnx.b, e->h, b, D, EPS), "add+ln");
         TRY(gemm(DEPI_PARTIAL, e->h, D, L.xq, D, D, ks_dd, e->part, D), "dec cross q");
-        a = MzDecAttn{};
-        a.q = e->part;
-        a.nq = ks_dd;
-        a.qstride = (long)b * D;
-        a.qbias = L.xq.b;
-        a.k = e->xkvbuf + (size_t)(2 * i) * nh * blk;
-        a.vt = e->xkvbuf + (size_t)(2 * i + 1) * nh * blk;
-        a.kv_b = (long)nl * 2 * nh * blk;
-        a.kv_h = blk;
-        a.vt_ld = TPAD;
-        a.L = TENC;
-        a.ctr = e->ctr;
-        a.done = e->done;
-        a.out = e->datt;
-        a.B = b;
-        a.nh = nh;
-        a.d = D;
-        a.nsplit = (TENC + XCHUNK - 1) / XCHUNK;
-        a.chunk = XCHUNK;
-        a.part = e->xpart;
-        a.counter = e->xcnt;
-        a.aslot = e->aslot + (size_t)i * nh;
-        a.sal = e->sal;
-        a.align = e->align;
-        a.na = e->na;
-        a.maxT = mt;
-        TRY(mz_dec_attn_launch(s, a), "cross attention");
+        TRY(attn(e->part, ks_dd, L.xq.b, e->xkvbuf + (size_t)(2 * i) * nh * blk, e->xkvbuf + (size_t)(2 * i + 1) * nh * blk,
+                 (long)nl * 2 * nh * blk, TENC, e->aslot + (size_t)i * nh),
+            "cross attention");
         TRY(gemm(DEPI_PARTIAL, e->datt, D, L.xo, D, D, ks_dd, e->part, D), "dec cross out-proj");
         TRY(mz_dec_add_ln_launch(s, e->x, e->part, ks_dd, (long)b * D, L.xo.b, L.ln3.w, L.ln3.b, e->h, b, D, EPS), "add+ln");
         TRY(gemm(DEPI_GELU_F16, e->h, D, L.fc1, F, D, 1, e->dff, F), "dec fc1");
@@ -603,12 +678,27 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
         const Ln& nx = i + 1 < nl ? e->decv[i + 1].ln1 : e->dln;
         TRY(mz_dec_add_ln_launch(s, e->x, e->part, ks_df, (long)b * D, L.fc2.b, nx.w, nx.b, e->h, b, D, EPS), "add+ln");
     }
-    // tied LM head, then the greedy choice; its last block advances the position
-    Lin head{e->emb, nullptr};
-    TRY(gemm(DEPI_F32, e->h, D, head, V, D, 1, e->logits, V), "lm head");
-    TRY(mz_dec_argmax_launch(s, e->logits, V, lang ? e->sup_lang : e->sup, e->tok, e->done, e->ctr, e->acnt, b, mt,
-                             prompt_len, e->eos, lang ? -1 : e->bs1, lang ? -1 : e->bs2, 1),
-        "argmax");
+    // tied LM head with the masked per-workgroup argmax, then the greedy choice, which advances the position
+    {
+        MzDec g{};
+        g.x = e->h;
+        g.ldx = D;
+        g.W = e->emb;
+        g.M = b;
+        g.N = V;
+        g.K = D;
+        g.ksplit = 1;
+        g.out = e->logits;
+        g.ldo = V;
+        g.ctr = e->ctr;
+        g.sup = lang ? e->sup_lang : e->sup;
+        g.bs1 = lang ? -1 : e->bs1;
+        g.bs2 = lang ? -1 : e->bs2;
+        g.prompt_len = prompt_len;
+        g.amax = e->amax;
+        TRY(mz_dec_gemm_launch(s, DEPI_LOGITS, g), "lm head");
+    }
+    TRY(mz_dec_argmax_launch(s, e->amax, (V + 31) / 32, e->tok, e->done, e->ctr, b, mt, prompt_len, e->eos), "argmax");
     return MZ_OK;
 }
 
@@ -616,6 +706,7 @@ extern "C" int mz_engine_step(mz_engine* e, int b, int lang, int prompt_len) {
     if (!e) return mz_fail(MZ_ERR_ARG, "mz_engine_step: null engine");
     if (!e->loaded) return mz_fail(MZ_ERR_STATE, "mz_engine_step: weights not loaded");
     if (b <= 0 || b > e->bmax) return mz_fail(MZ_ERR_ARG, "mz_engine_step: %d rows (bmax %d)", b, e->bmax);
+    if (int r = take_position(e)) return r;
     return step_impl(e, b, lang, prompt_len);
 }
 
@@ -638,7 +729,10 @@ extern "C" int mz_engine_capture(mz_engine* e, int b, int prompt_len) {
         e->graph = nullptr;
     }
     if (int r = mz_graph_begin(e->c)) return r;
+    const bool prof = e->prof_on;
+    e->prof_on = false;  // events are not recorded into the graph
     int rs = step_impl(e, b, 0, prompt_len);
+    e->prof_on = prof;
     mz_graph* g = nullptr;
     int re = mz_graph_end(e->c, &g);
     if (rs) {
@@ -654,7 +748,10 @@ extern "C" int mz_engine_capture(mz_engine* e, int b, int prompt_len) {
 
 extern "C" int mz_engine_replay(mz_engine* e) {
     if (!e || !e->graph) return mz_fail(MZ_ERR_STATE, "mz_engine_replay: no captured step");
-    return mz_graph_launch(e->c, e->graph);
+    if (int r = take_position(e)) return r;
+    hipStream_t s = e->c->stream;
+    PROF(MZ_K_STEP, mz_graph_launch(e->c, e->graph) ? hipErrorUnknown : hipSuccess, "hipGraphLaunch");
+    return MZ_OK;
 }
 
 extern "C" int mz_engine_buffer(mz_engine* e, int which, uint64_t* dptr, size_t* bytes) {
@@ -695,11 +792,17 @@ extern "C" int mz_engine_free(mz_engine* e) {
     if (!e) return MZ_OK;
     if (e->graph) mz_graph_free(e->graph);
     hipStreamSynchronize(e->c->stream);
+    for (auto& r : e->recs) {
+        hipEventDestroy(r.a);
+        hipEventDestroy(r.b);
+    }
+    for (hipEvent_t x : e->evpool) hipEventDestroy(x);
+    if (e->align_host) hipHostFree(e->align_host);
     for (void* p : {(void*)e->arena, (void*)e->mel, (void*)e->melT, (void*)e->h1, (void*)e->ex, (void*)e->hb,
                     (void*)e->qkvh, (void*)e->att, (void*)e->ff, (void*)e->trace, (void*)e->xkvbuf, (void*)e->tok,
                     (void*)e->done, (void*)e->ctr, (void*)e->x, (void*)e->q, (void*)e->h, (void*)e->datt,
-                    (void*)e->dff, (void*)e->kc, (void*)e->vct, (void*)e->logits, (void*)e->align, (void*)e->xpart,
-                    (void*)e->xcnt, (void*)e->acnt, (void*)e->sal, (void*)e->aslot, (void*)e->sup, (void*)e->sup_lang,
+                    (void*)e->dff, (void*)e->kc, (void*)e->vc, (void*)e->logits, (void*)e->align, (void*)e->amax,
+                    (void*)e->aslot, (void*)e->sup, (void*)e->sup_lang,
                     (void*)e->part})
         if (p) mz_free(e->c, (uint64_t)(uintptr_t)p);
     delete e;
@@ -708,13 +811,17 @@ extern "C" int mz_engine_free(mz_engine* e) {
 
 // ------------------------------------------------------------------ batch transcription (src/transcribe.rs:104-167)
 
-extern "C" int mz_transcribe(mz_engine* e, const float* mels, const int32_t* frames, int n, const int32_t* prompt,
-                             int prompt_len, int detect, int use_graph, int max_new, int half_align, int32_t* seq,
-                             int32_t* seq_len, float* ts, int32_t* langs, mz_times* times) {
+static int transcribe_impl(mz_engine* e, const float* mels, bool on_device, const int32_t* frames, int n,
+                           const int32_t* prompt, int prompt_len, int detect, int use_graph, int max_new,
+                           int half_align, int32_t* seq, int32_t* seq_len, float* ts, int32_t* langs,
+                           mz_times* times) {
     using clk = std::chrono::steady_clock;
     if (!e || !mels || !frames || !prompt || !seq || !seq_len || !ts || !langs)
         return mz_fail(MZ_ERR_ARG, "mz_transcribe: null argument");
     if (n <= 0 || n > e->bmax) return mz_fail(MZ_ERR_ARG, "mz_transcribe: %d clips (bmax %d)", n, e->bmax);
+    for (int c = 0; c < n; c++)
+        if (frames[c] < 0 || frames[c] > NFR)
+            return mz_fail(MZ_ERR_ARG, "mz_transcribe: clip %d has %d frames (0..%d)", c, frames[c], NFR);
     const int mt = e->dm.max_t, nm = e->dm.n_mels, eos = e->eos, np = prompt_len;
     auto sec = [](clk::time_point a) { return std::chrono::duration<double>(clk::now() - a).count(); };
     mz_times tm{};
@@ -722,7 +829,7 @@ extern "C" int mz_transcribe(mz_engine* e, const float* mels, const int32_t* fra
     auto t0 = clk::now();
     for (int g0 = 0; g0 < n; g0 += e->eg) {
         const int gn = std::min(e->eg, n - g0);
-        if (int r = mz_engine_encode(e, mels + (size_t)g0 * nm * NFR, gn, g0)) return r;
+        if (int r = encode_impl(e, mels + (size_t)g0 * nm * NFR, on_device, gn, g0)) return r;
     }
     if (int r = mz_sync(e->c)) return r;
     tm.enc = sec(t0);
@@ -745,7 +852,7 @@ extern "C" int mz_transcribe(mz_engine* e, const float* mels, const int32_t* fra
     }
     std::vector<int32_t> dn(n);
     while (steps < limit) {
-        if (int r = use_graph ? mz_engine_replay(e) : step_impl(e, n, 0, np)) return r;
+        if (int r = use_graph ? mz_engine_replay(e) : mz_engine_step(e, n, 0, np)) return r;
         steps++;
         if (steps % 8 == 0 && steps >= np) {
             if (int r = mz_download(e->c, dn.data(), (uint64_t)(uintptr_t)e->done, (size_t)n * 4)) return r;
@@ -760,8 +867,9 @@ extern "C" int mz_transcribe(mz_engine* e, const float* mels, const int32_t* fra
     std::vector<int32_t> toks((size_t)n * mt);
     if (int r = mz_download(e->c, toks.data(), (uint64_t)(uintptr_t)e->tok, toks.size() * 4)) return r;
     const size_t row = (size_t)e->na * TENC;
-    std::vector<uint16_t> wh;
-    std::vector<float> w, jt;
+    // sequence lengths, then the alignment rows of every clip into pinned memory in one batch of copies
+    std::vector<int> nseq(n), nrows(n);
+    std::vector<size_t> off(n + 1, 0);
     for (int c = 0; c < n; c++) {
         const int32_t* t = &toks[(size_t)c * mt];
         int n_seq = std::min(steps + 1, mt);
@@ -771,26 +879,71 @@ extern "C" int mz_transcribe(mz_engine* e, const float* mels, const int32_t* fra
                 break;
             }
         n_seq = std::min(n_seq, steps + 1);
+        nseq[c] = n_seq;
+        nrows[c] = std::max(n_seq - 1 - np, 0);
+        off[c + 1] = off[c] + (size_t)nrows[c] * row;
+    }
+    if (off[n] * 2 > e->align_host_bytes) {
+        if (e->align_host) hipHostFree(e->align_host);
+        e->align_host = nullptr;
+        e->align_host_bytes = 0;
+        const size_t want = (size_t)e->bmax * mt * row * 2;
+        TRY(hipHostMalloc((void**)&e->align_host, want, hipHostMallocDefault), "hipHostMalloc");
+        e->align_host_bytes = want;
+    }
+    for (int c = 0; c < n; c++)
+        if (nrows[c] > 0)
+            TRY(hipMemcpyAsync(e->align_host + off[c], e->align + ((size_t)c * mt + np) * row,
+                               (size_t)nrows[c] * row * 2, hipMemcpyDeviceToHost, e->c->stream),
+                "align download");
+    if (int r = mz_sync(e->c)) return r;
+    // token timestamps per clip (median filter + DTW on the host), clips in parallel
+    std::vector<std::vector<float>> jts(n);
+    std::vector<int> rcs(n, MZ_OK);
+    std::atomic<int> next{0};
+    auto work = [&]() {
+        for (int c; (c = next.fetch_add(1)) < n;) {
+            if (nrows[c] <= 0) continue;
+            jts[c].resize(nrows[c]);
+            rcs[c] = mz_jump_times_f16(e->align_host + off[c], nrows[c], e->na, TENC, frames[c] / 2, 7, half_align,
+                                       jts[c].data());
+        }
+    };
+    const int nth = std::max(1, std::min({n, (int)std::thread::hardware_concurrency(), 16}));
+    std::vector<std::thread> pool;
+    for (int t = 1; t < nth; t++) pool.emplace_back(work);
+    work();
+    for (auto& th : pool) th.join();
+    for (int c = 0; c < n; c++) {
+        if (rcs[c]) return rcs[c];
+        const int32_t* t = &toks[(size_t)c * mt];
+        const int n_seq = nseq[c];
         for (int k = 0; k < mt; k++) seq[(size_t)c * mt + k] = k < n_seq ? t[k] : 0;
         seq_len[c] = n_seq;
         float* tc = ts + (size_t)c * mt;
         std::fill(tc, tc + mt, 0.f);
-        const int rows = std::max(n_seq - 1 - np, 0);
+        const int rows = nrows[c];
         if (rows > 0) {
-            wh.resize((size_t)rows * row);
-            if (int r = mz_download(e->c, wh.data(), (uint64_t)(uintptr_t)(e->align + ((size_t)c * mt + np) * row),
-                                    wh.size() * 2))
-                return r;
-            w.resize(wh.size());
-            for (size_t k = 0; k < wh.size(); k++) w[k] = mz_h2f_host(wh[k]);
-            jt.resize(rows);
-            if (int r = mz_jump_times(w.data(), rows, e->na, TENC, frames[c] / 2, 7, half_align, jt.data())) return r;
-            for (int k = 0; k < rows; k++) tc[np + k] = jt[k];
-            tc[n_seq - 1] = jt[rows - 1];
+            for (int k = 0; k < rows; k++) tc[np + k] = jts[c][k];
+            tc[n_seq - 1] = jts[c][rows - 1];
         }
         langs[c] = lg[c];
     }
     tm.post = sec(t0);
     if (times) *times = tm;
     return MZ_OK;
+}
+
+extern "C" int mz_transcribe(mz_engine* e, const float* mels, const int32_t* frames, int n, const int32_t* prompt,
+                             int prompt_len, int detect, int use_graph, int max_new, int half_align, int32_t* seq,
+                             int32_t* seq_len, float* ts, int32_t* langs, mz_times* times) {
+    return transcribe_impl(e, mels, false, frames, n, prompt, prompt_len, detect, use_graph, max_new, half_align, seq,
+                           seq_len, ts, langs, times);
+}
+
+extern "C" int mz_transcribe_device(mz_engine* e, uint64_t mels, const int32_t* frames, int n, const int32_t* prompt,
+                                    int prompt_len, int detect, int use_graph, int max_new, int half_align,
+                                    int32_t* seq, int32_t* seq_len, float* ts, int32_t* langs, mz_times* times) {
+    return transcribe_impl(e, (const float*)(uintptr_t)mels, true, frames, n, prompt, prompt_len, detect, use_graph,
+                           max_new, half_align, seq, seq_len, ts, langs, times);
 }

@@ -165,7 +165,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(const MzGemm p) {
                     const int g = m / MZ_TENC, t = m - g * MZ_TENC;
                     const int blk = n >> 6, dim = n & 63;
                     f16* base = p.heads + ((long)(p.slot0 + g) * p.blocks_per_clip + blk) * (MZ_TPAD * MZ_HD);
-                    if ((blk / p.nh) % p.kind == p.kind - 1) {
+                    if (p.kind == 3 && blk / p.nh == 2) {  // encoder v: transposed for the P.V product
 #pragma unroll
                         for (int e = 0; e < 4; e++) base[(long)(dim + e) * MZ_TPAD + t] = (f16)v[e];
                     } else {

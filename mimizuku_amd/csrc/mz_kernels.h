@@ -14,7 +14,7 @@ enum MzEpi {
     EPI_GELU_F16 = 1,   // out f16 [M][ldo] = gelu(acc + bias)
     EPI_RESID_F32 = 2,  // out f32 [M][ldo] += acc + bias        (residual add fused into the producing GEMM)
     EPI_GELU_POS = 3,   // out f32 [M][ldo] = gelu(acc + bias) + pos[m % 1500][n]   (conv2 -> residual stream)
-    EPI_HEADS = 4,      // head-major scatter: K-like blocks [1536][64], V-like blocks transposed [64][1536]
+    EPI_HEADS = 4,      // head-major scatter into [1536][64] tiles (encoder v transposed [64][1536])
 };
 
 struct MzGemm {
@@ -31,7 +31,8 @@ struct MzGemm {
     const f16* pos;
     // EPI_HEADS: column n belongs to 64-wide block blk = n / 64 and row m = g * 1500 + t to clip g; the block's
     // 1536 x 64 tile lives at heads + ((slot0 + g) * blocks_per_clip + blk) * 1536 * 64. kind 3: blocks ordered
-    // [q|k|v][head], kind 2: [layer][k|v][head]; the last member of each group (v) is stored transposed [64][1536].
+    // [q|k|v][head] (encoder self-attention; v stored transposed [64][1536] for the P.V matrix product), kind 2:
+    // [layer][k|v][head] (decoder cross-attention; every tile row-major [1536][64]).
     f16* heads;
     int blocks_per_clip, nh, kind, slot0;
 };
@@ -53,12 +54,16 @@ hipError_t mz_add_layernorm_launch(hipStream_t s, float* x, const f16* d, const 
 hipError_t mz_mel_transpose_launch(hipStream_t s, const float* mel, f16* melT, int G, int nm);
 
 // ---------------------------------------------------------------- decoder step
+// Position: ctr[0] = position of the next step; the step's first kernel (embed) copies it to ctr[1], the later
+// kernels read ctr[1], the last one (argmax) writes ctr[0] = ctr[1] + 1.
+#define MZ_MAX_PARTS 16  // split-K partials summed by dec_add_ln
+
 // skinny GEMM for decode batches: rows m < M of x (f16, row stride ldx, M <= 32 per m-tile) times W[N][K]
 enum MzDecEpi {
     DEPI_PARTIAL = 0,  // part[ks][m][n] (f32), ks = blockIdx.y (split-K)
     DEPI_GELU_F16 = 1, // out f16 [m][ldo] = gelu(acc + bias)
-    DEPI_F32 = 2,      // out f32 [m][ldo] = acc (+ bias)
-    DEPI_QKV = 3,      // q -> qout f32 [m][d] (+bias); k, v (+bias) -> self cache at position ctr[0]
+    DEPI_LOGITS = 2,   // out f32 [m][ldo] = acc, and amax[blockIdx.x][m] = masked (max, lowest id) of the 32 columns
+    DEPI_QKV = 3,      // q -> out f32 [m][d] (+bias); k, v (+bias) -> self cache rows at position ctr[1]
     DEPI_F16 = 4,      // out f16 [m][ldo] = acc + bias
 };
 struct MzDec {
@@ -69,11 +74,15 @@ struct MzDec {
     int M, N, K, ksplit;
     void* out;
     long ldo;
-    // DEPI_QKV
-    f16* kc;   // [bmax][nh][maxT][64] of this layer
-    f16* vct;  // [bmax][nh][64][maxT] of this layer
     const int* ctr;
+    // DEPI_QKV: this layer's cache, [bmax][nh][maxT][64] for both k and v
+    f16* kc;
+    f16* vc;
     int maxT, d;
+    // DEPI_LOGITS: mask (nonzero = never chosen), begin-suppressed ids at the first generated position, partials
+    const unsigned char* sup;
+    int bs1, bs2, prompt_len;
+    void* amax;  // int2 {float bits, id} [grid.x][M]
 };
 hipError_t mz_dec_gemm_launch(hipStream_t s, int epi, const MzDec& g);
 
@@ -83,35 +92,29 @@ struct MzDecAttn {
     int nq;
     long qstride;
     const f16* qbias;
-    // keys of (b, head): k + b * kv_b + head * kv_h, rows of 64 halves; V^T likewise at vt, rows of vt_ld keys
+    // keys and values of (b, head): rows of 64 halves at k + b * kv_b + head * kv_h (v likewise)
     const f16* k;
-    const f16* vt;
-    long kv_b, kv_h;   // element strides of a row b and a head (same for k and vt)
-    int vt_ld;         // keys per row of V^T
-    int L;             // keys (cross) or -1: ctr[0] + 1 (self)
+    const f16* v;
+    long kv_b, kv_h;
+    int L;             // keys (cross, <= 1536) or -1: position + 1 (self)
     const int* ctr;
     const int* done;
     f16* out;          // [B][d]
     int B, nh, d;
-    int nsplit, chunk;  // key chunks per (b, head)
-    // split combine scratch
-    float* part;        // [B * nh][nsplit][66]
-    unsigned* counter;  // [B * nh]
-    // alignment-head capture (cross only, may be null)
-    const int* aslot;   // [nl * nh] for this layer: slot or -1 (already offset to the layer)
-    float* sal;         // [B][na][1536] raw scores
-    f16* align;         // [bmax][maxT][na][1500]
-    int na, maxT;
+    int maxT;
+    // alignment-head capture (cross only, may be null): slot of each head of this layer or -1
+    const int* aslot;
+    f16* align;        // [bmax][maxT][na][1500]
+    int na;
 };
 hipError_t mz_dec_attn_launch(hipStream_t s, const MzDecAttn& a);
 
 // x[b] += sum_s parts[s][b] + bias; y[b] = LN(x[b])  (the residual add fused with the next layer norm)
 hipError_t mz_dec_add_ln_launch(hipStream_t s, float* x, const float* parts, int nparts, long part_stride,
                                 const f16* bias, const f16* w, const f16* b, f16* y, int rows, int dim, float eps);
-// x[b] = emb[tok[b * maxT + p]] + pe[p] (fp32); y[b] = LN(x[b])
-hipError_t mz_dec_embed_ln_launch(hipStream_t s, const int* tok, const int* ctr, const f16* emb, const f16* pe,
-                                  float* x, const f16* w, const f16* b, f16* y, int rows, int dim, int maxT, float eps);
-// greedy choice of token p + 1 (kernels/whisper.cu:451-493 semantics) and, by the last block, ctr[0] += 1
-hipError_t mz_dec_argmax_launch(hipStream_t s, const float* logits, int V, const unsigned char* sup, int* tok, int* done,
-                                int* ctr, unsigned* counter, int B, int maxT, int prompt_len, int eos, int bs1, int bs2,
-                                int advance);
+// ctr[1] = ctr[0]; x[b] = emb[tok[b * maxT + p]] + pe[p] (fp32); y[b] = LN(x[b])
+hipError_t mz_dec_embed_ln_launch(hipStream_t s, const int* tok, int* ctr, const f16* emb, const f16* pe, float* x,
+                                  const f16* w, const f16* b, f16* y, int rows, int dim, int maxT, float eps);
+// greedy choice of token p + 1 (kernels/whisper.cu:451-493 semantics) from the LM head partials; ctr[0] = p + 1
+hipError_t mz_dec_argmax_launch(hipStream_t s, const int2* amax, int nblk, int* tok, int* done, int* ctr, int B,
+                                int maxT, int prompt_len, int eos);

@@ -243,6 +243,24 @@ class Engine:
         assert m.ndim == 3 and m.shape[1:] == (self.dims.n_mels, NFRAMES), m.shape
         check(L.lib().mz_engine_encode(self.h, ptr(m), m.shape[0], slot0))
 
+    def encode_device(self, mels: int, n: int, slot0: int = 0):
+        """Encoder for n clips whose log-mel f32 [n][n_mels][3000] is already in device memory at address mels."""
+        check(L.lib().mz_engine_encode_device(self.h, mels, n, slot0))
+
+    # ---- kernel timing (events on the engine's stream)
+    def profile(self, on: bool = True):
+        """Clear the timing records and switch event timing of encoder launches and step replays on or off."""
+        check(L.lib().mz_engine_profile(self.h, int(on)))
+
+    def profile_read(self) -> dict:
+        """{kernel class: (total ms, launches)} over the records since the last profile() call."""
+        out = {}
+        for i, name in enumerate(L.K_NAMES):
+            ms, n = C.c_double(), C.c_int()
+            check(L.lib().mz_engine_profile_read(self.h, i, C.byref(ms), C.byref(n)))
+            out[name] = (ms.value, n.value)
+        return out
+
     def reset(self, prompts):
         p = np.ascontiguousarray(np.array(prompts, np.int32))
         check(L.lib().mz_engine_reset(self.h, ptr(p), p.shape[0], p.shape[1]))

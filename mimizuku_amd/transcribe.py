@@ -61,17 +61,24 @@ class Times:
     steps: int = 0
 
 
-def transcribe(e: Engine, mels: np.ndarray, p: Prompt, frames=None, graph: bool = True, max_new: int = 0,
-               half_align: bool = True) -> tuple[list[Decoded], Times]:
-    """Encode and decode up to e.bmax clips (log-mel f32 [n][n_mels][3000]); returns their tokens with timestamps.
+def transcribe(e: Engine, mels, p: Prompt, frames=None, graph: bool = True, max_new: int = 0,
+               half_align: bool = True, n: int | None = None) -> tuple[list[Decoded], Times]:
+    """Encode and decode up to e.bmax clips; returns their tokens with timestamps (src/transcribe.rs:104-167).
 
+    mels is log-mel f32 [n][n_mels][3000], either a host array or, with n given, the address of such an array in
+    device memory (then nothing crosses PCIe before the encoder).
     max_new > 0 caps the generated tokens (the reference decodes until every row ends or max_t - 1 steps).
     half_align rounds the timestamp arithmetic through fp16 where an fp16 model does (src/align.rs).
     """
-    m = np.ascontiguousarray(mels, np.float32)
-    n = m.shape[0]
-    if m.shape[1:] != (e.dims.n_mels, NFRAMES):
-        raise MzError(f"mels must be [n][{e.dims.n_mels}][{NFRAMES}], got {m.shape}")
+    on_device = isinstance(mels, int)
+    if on_device:
+        if n is None:
+            raise MzError("transcribe: the clip count n is needed with device-resident mels")
+    else:
+        m = np.ascontiguousarray(mels, np.float32)
+        n = m.shape[0]
+        if m.shape[1:] != (e.dims.n_mels, NFRAMES):
+            raise MzError(f"mels must be [n][{e.dims.n_mels}][{NFRAMES}], got {m.shape}")
     fr = np.ascontiguousarray(np.full(n, NFRAMES, np.int32) if frames is None else np.array(frames, np.int32))
     prompt = np.array(p.tokens(p.lang if p.lang is not None else p.sot), np.int32)
     mt = e.dims.max_t
@@ -80,9 +87,12 @@ def transcribe(e: Engine, mels: np.ndarray, p: Prompt, frames=None, graph: bool 
     ts = np.zeros((n, mt), np.float32)
     langs = np.zeros(n, np.int32)
     tm = L.Times()
-    check(L.lib().mz_transcribe(e.h, ptr(m), ptr(fr), n, ptr(prompt), len(prompt), int(p.detect()), int(graph),
-                                int(max_new), int(half_align), ptr(seq), ptr(seq_len), ptr(ts), ptr(langs),
-                                C.byref(tm)))
+    args = (ptr(fr), n, ptr(prompt), len(prompt), int(p.detect()), int(graph), int(max_new), int(half_align),
+            ptr(seq), ptr(seq_len), ptr(ts), ptr(langs), C.byref(tm))
+    if on_device:
+        check(L.lib().mz_transcribe_device(e.h, mels, *args))
+    else:
+        check(L.lib().mz_transcribe(e.h, ptr(m), *args))
     out = [Decoded(int(langs[i]), seq[i, :seq_len[i]].tolist(), ts[i, :seq_len[i]].tolist()) for i in range(n)]
     return out, Times(tm.enc, tm.dec, tm.post, tm.steps)
 

@@ -1,0 +1,179 @@
+"""GPU parity of the whole path (engine + transcription loop) on the Whisper-tiny geometry, against the oracle and
+the golden vectors transformers wrote (tests/golden/*.npz).
+
+* encoder: every layer checked layer-local — the oracle's layer applied to the engine's own fp32 input of that layer
+  — at max-abs error <= 2e-3 x RMS; the conv stem and the final LayerNorm likewise;
+* decoder: teacher-forced on the golden sequence, logits and alignment-head weights against the oracle at every
+  step, and the greedy choice equal wherever the oracle's top-2 margin exceeds 1e-2;
+* the batch API (graph replay) reproduces the golden token sequences and 20 ms-grid timestamps, and graph replay is
+  bit-identical to eager steps.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from mimizuku_amd import _lib as L
+from mimizuku_amd import model, synth, transcribe
+from oracle import whisper_ref as R
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+G = synth.TINY
+TOL = 2e-3
+MARGIN = 1e-2
+PROMPT_EN = [50258, 50259, 50359, 50363]
+
+
+def rel_err(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return np.abs(got - ref).max() / np.sqrt((ref ** 2).mean())
+
+
+class Case:
+    def __init__(self, name):
+        self.name = name
+        fx = np.load(os.path.join(GOLDEN, f"{name}.npz"))
+        self.fx = fx
+        self.W = synth.random_weights(G, seed=int(fx["seed"]), bias_std=float(fx["bias_std"]),
+                                      ln_std=float(fx["ln_std"]))
+        assert synth.weights_digest(self.W) == str(fx["weights_digest"])
+        self.Wf = {k: v.astype(np.float32) for k, v in self.W.items()}
+        self.n = int(fx["n_clips"])
+        self.mel = synth.synthetic_mel(self.n, G.n_mels, seed=int(fx["mel_seed"]))
+        self.gen = synth.generation_config(G)
+        self.detect = bool(fx["detect"])
+        self.seq = fx["sequences"]
+        self.dims = model.Dims(G.d, G.ff, G.nh, G.enc_layers, G.dec_layers, G.n_mels, G.vocab, G.max_t)
+        self.gc = model.GenCfg.from_dict(self.gen, self.dims)
+        # the oracle teacher-forced on the golden sequence (equal to its own greedy run, pinned in test_oracle.py)
+        self.ref = R.greedy(self.Wf, G, self.gen, self.mel, PROMPT_EN, self.seq.shape[1] - 4, detect=self.detect,
+                            teacher=self.seq)
+
+    def engine(self, ctx, bmax=None):
+        e = model.Engine(ctx, self.dims, self.gc, bmax or self.n, self.n)
+        e.load(self.W)
+        return e
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = model.Context(0)
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module", params=["tiny_hfinit", "tiny_bias_detect"])
+def case(request):
+    return Case(request.param)
+
+
+def test_encoder_layer_local(ctx, case):
+    e = case.engine(ctx)
+    e.set_trace(True)
+    e.encode(case.mel, 0)
+    tr = e.trace(case.n)  # [L][n][1500][d] inputs of every layer
+    xl = e.read(L.BUF_ENC_X, np.float32, (case.n, 1500, G.d))  # residual after the last layer
+    out = e.enc_out(case.n).astype(np.float32)
+    W = case.Wf
+    for c in range(case.n):
+        m16 = case.mel[c].astype(np.float16).astype(np.float32)  # the engine takes the mel to fp16 first
+        errs = [rel_err(tr[0, c], R.conv_stem(m16, W))]
+        for i in range(G.enc_layers):
+            nxt = tr[i + 1, c] if i + 1 < G.enc_layers else xl[c]
+            errs.append(rel_err(nxt, R.encoder_layer(tr[i, c], W, i, G.nh)))
+        errs.append(rel_err(out[c], R.layer_norm(xl[c], W["model.encoder.layer_norm.weight"],
+                                                 W["model.encoder.layer_norm.bias"])))
+        print(case.name, c, ["%.2e" % x for x in errs])
+        assert max(errs) < TOL, errs
+    e.close()
+
+
+def test_decoder_teacher_forced(ctx, case):
+    """Reset with the whole golden sequence as the prompt: every step then feeds the golden token, and the logits
+    and alignment rows of each position are compared with the oracle's at that position."""
+    e = case.engine(ctx)
+    e.encode(case.mel, 0)
+    seq = case.seq.astype(np.int32)
+    T = seq.shape[1]
+    e.reset(seq)
+    sup = set(case.gen["suppress_tokens"])
+    bsup = case.gen["begin_suppress_tokens"]
+    worst = 0.0
+    for p in range(T - 1):
+        e.step(case.n, False, T)
+        if p + 1 < 4:
+            continue
+        lg = e.logits()[:case.n]
+        ref = case.ref["logits"][p + 1 - 4]
+        worst = max(worst, rel_err(lg, ref))
+        for b in range(case.n):
+            first = p + 1 == 4
+            if case.ref["margins"][p + 1 - 4][b] > MARGIN:
+                assert R.choose(lg[b], sup, bsup, first, 50257, False) == int(seq[b, p + 1]), (p, b)
+    print(case.name, "logits max-abs / RMS", worst)
+    assert worst < 2e-2
+    al = e.align()[:case.n, :T - 1].astype(np.float32)  # [n][rows][heads][1500]
+    probs = case.ref["probs"]  # [n][rows][L][nh][1500]
+    for s, (l, h) in enumerate(case.gen["alignment_heads"]):
+        ref = probs[:, :T - 1, l, h]
+        err = np.abs(al[:, :, s] - ref).max()
+        assert err < 1e-3 * ref.max(), (s, err)
+        np.testing.assert_allclose(al[:, :, s].sum(-1), 1.0, atol=3e-3)
+    assert e.position() == T - 1
+    e.close()
+
+
+def test_transcribe_matches_golden(ctx, case):
+    e = case.engine(ctx)
+    p = transcribe.Prompt(e.gc, "auto" if case.detect else "en")
+    out, tm = transcribe.transcribe(e, case.mel, p, max_new=case.seq.shape[1] - 4, half_align=False)
+    for b, d in enumerate(out):
+        if case.detect:
+            assert d.lang == int(case.seq[b, 1])
+        want = case.seq[b].tolist()
+        # identical up to the first generating step whose oracle margin is within 1e-2 (where a different but
+        # equally likely token is allowed and the rest of the sequence follows from it)
+        low = [s for s, m in enumerate(case.ref["margins"][:, b]) if m <= MARGIN]
+        upto = 4 + (low[0] if low else len(want))
+        assert d.seq[:upto] == want[:upto], (b, d.seq, want)
+        if not low:
+            assert d.seq == want[:len(d.seq)]
+            np.testing.assert_array_equal(np.array(d.ts, np.float32), case.fx["token_timestamps"][b][:len(d.ts)])
+    assert tm.steps == case.seq.shape[1] - 1
+    e.close()
+
+
+def test_graph_replay_equals_eager(ctx, case):
+    res = []
+    for graph in (True, False):
+        e = case.engine(ctx)
+        p = transcribe.Prompt(e.gc, "auto" if case.detect else "en")
+        out, _ = transcribe.transcribe(e, case.mel, p, graph=graph, max_new=20)
+        res.append((out, e.logits(), e.align(), e.dec_x()))
+        e.close()
+    (o1, l1, a1, x1), (o2, l2, a2, x2) = res
+    assert [d.seq for d in o1] == [d.seq for d in o2]
+    assert [d.ts for d in o1] == [d.ts for d in o2]
+    np.testing.assert_array_equal(l1, l2)
+    np.testing.assert_array_equal(a1, a2)
+    np.testing.assert_array_equal(x1, x2)
+
+
+def test_step_beyond_the_cache_is_refused(ctx):
+    case_dims = model.Dims(G.d, G.ff, G.nh, 1, 1, G.n_mels, G.vocab, 16)
+    gen = synth.generation_config(G, align_heads=[[0, 0]])
+    gc = model.GenCfg.from_dict(gen, case_dims)
+    W = {k: v for k, v in synth.random_weights(synth.Geometry(G.d, G.ff, G.nh, 1, 1, G.n_mels, G.vocab, 16)).items()}
+    e = model.Engine(ctx, case_dims, gc, 1, 1)
+    e.load(W)
+    e.encode(synth.synthetic_mel(1, G.n_mels), 0)
+    e.reset([PROMPT_EN])
+    for _ in range(15):
+        e.step(1, False, 4)
+    with pytest.raises(L.MzError, match="cache"):
+        e.step(1, False, 4)
+    assert e.position() == 15
+    e.close()

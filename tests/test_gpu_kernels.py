@@ -1,0 +1,273 @@
+"""GPU parity of the individual kernels through the C ABI, against float64 closed forms on the same fp16 inputs (or
+the oracle's functions), at small shapes and at the full large-v3 shapes with subsampled checks.
+
+Tolerances: an fp16 output is the exact result rounded to fp16 within one ulp (assert_f16); an fp32 output, and the
+attention output (whose P operand the kernel rounds to fp16), within max-abs error <= 2e-3 x RMS of the reference.
+"""
+import numpy as np
+import pytest
+
+from mimizuku_amd import _lib as L
+from mimizuku_amd import model
+from oracle import whisper_ref as R
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+TPAD = 1536
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = model.Context(0)
+    yield c
+    c.close()
+
+
+def rel_err(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return np.abs(got - ref).max() / np.sqrt((ref ** 2).mean())
+
+
+def assert_f16(got, ref, ulps=1.0):
+    """An fp16 output must be the exact value rounded to fp16, within `ulps` units in the last place of that value
+    (correct rounding is half an ulp; fp32 accumulation order may flip a rounding), plus 1e-5 x RMS for results that
+    cancel to near zero."""
+    ref = np.asarray(ref, np.float64)
+    got = np.asarray(got, np.float64)
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    bound = ulps * ulp + 1e-5 * np.sqrt((ref ** 2).mean())
+    bad = np.abs(got - ref) > bound
+    assert not bad.any(), f"{bad.sum()} of {bad.size} outside {ulps} ulp: worst at {np.argwhere(bad)[:3].tolist()}"
+
+
+def f16(rng, shape, scale=1.0):
+    return (rng.standard_normal(shape, dtype=np.float32) * scale).astype(np.float16)
+
+
+# ---------------------------------------------------------------- encoder attention
+
+def pack_qkvh(q, k, v):
+    """q, k, v [G][nh][1500][64] fp16 -> [G][3][nh][1536 * 64] with v transposed, zero padded."""
+    G, nh = q.shape[:2]
+    out = np.zeros((G, 3, nh, TPAD * 64), np.float16)
+    for a, x in enumerate((q, k)):
+        t = np.zeros((G, nh, TPAD, 64), np.float16)
+        t[:, :, :1500] = x
+        out[:, a] = t.reshape(G, nh, -1)
+    t = np.zeros((G, nh, 64, TPAD), np.float16)
+    t[:, :, :, :1500] = v.transpose(0, 1, 3, 2)
+    out[:, 2] = t.reshape(G, nh, -1)
+    return out
+
+
+def run_attention(ctx, q, k, v):
+    G, nh = q.shape[:2]
+    dq = ctx.upload_new(pack_qkvh(q, k, v))
+    do = ctx.alloc(G * 1500 * nh * 64 * 2)
+    L.check(L.lib().mz_enc_attention(ctx.h, dq, do, G, nh))
+    out = ctx.download(do, (G, 1500, nh, 64), np.float16)
+    ctx.free(dq)
+    ctx.free(do)
+    return out.transpose(0, 2, 1, 3)  # [G][nh][1500][64]
+
+
+def attention64(q, k, v):
+    return R.attention(q, k, v, 0.125, dtype=np.float64)
+
+
+def test_enc_attention_small(ctx):
+    rng = np.random.default_rng(10)
+    q, k, v = (f16(rng, (1, 2, 1500, 64)) for _ in range(3))
+    out = run_attention(ctx, q, k, v)
+    ref = attention64(q, k, v)
+    assert rel_err(out, ref) < TOL
+    # a transposed V (a plausible layout mistake) is far outside the bar
+    assert rel_err(out, attention64(q, k, v[..., ::-1])) > 0.1
+
+
+def test_enc_attention_peaked_scores(ctx):
+    """Large logits (scale 4 x N(0,1) inputs): the online max/rescale path dominates."""
+    rng = np.random.default_rng(11)
+    q, k = f16(rng, (1, 1, 1500, 64), 4.0), f16(rng, (1, 1, 1500, 64), 4.0)
+    v = f16(rng, (1, 1, 1500, 64))
+    out = run_attention(ctx, q, k, v)
+    assert rel_err(out, attention64(q, k, v)) < TOL
+
+
+def test_enc_attention_large_v3_shape(ctx):
+    """8 clips x 20 heads x 1500 x 1500, head 64 (the encoder group's attention); every (clip, head) checked on 48
+    query rows spread over the window, including the last ones of the padded tile."""
+    rng = np.random.default_rng(12)
+    shape = (8, 20, 1500, 64)
+    q, k, v = (f16(rng, shape) for _ in range(3))
+    out = run_attention(ctx, q, k, v)
+    rows = np.r_[np.arange(0, 1500, 37), 1496, 1497, 1498, 1499]
+    ref = attention64(q[:, :, rows], k, v)
+    assert rel_err(out[:, :, rows], ref) < TOL
+    assert np.isfinite(out).all()
+
+
+# ---------------------------------------------------------------- GEMMs
+
+def linear_args(**kw):
+    a = L.LinearArgs()
+    for k_, v_ in kw.items():
+        setattr(a, k_, v_)
+    return a
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 64), (7, 100, 384), (32, 1280, 1280), (33, 96, 128), (3000, 768, 384),
+                                   (1500, 1284, 448)])
+def test_gemm_f16(ctx, m, n, k):
+    rng = np.random.default_rng(m * 7 + n)
+    x, w, b = f16(rng, (m, k)), f16(rng, (n, k), 0.05), f16(rng, (n,), 0.1)
+    dx, dw, db = ctx.upload_new(x), ctx.upload_new(w), ctx.upload_new(b)
+    dy = ctx.alloc(m * n * 2)
+    L.check(L.lib().mz_gemm(ctx.h, dx, k, dw, dy, n, m, n, k, db))
+    y = ctx.download(dy, (m, n), np.float16)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T + b
+    assert_f16(y, ref)
+    for p in (dx, dw, db, dy):
+        ctx.free(p)
+
+
+def test_gemm_epilogues(ctx):
+    rng = np.random.default_rng(3)
+    m, n, k = 3000, 512, 640
+    x, w, b = f16(rng, (m, k)), f16(rng, (n, k), 0.05), f16(rng, (n,), 0.1)
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    pos = f16(rng, (1500, n))
+    acc = x.astype(np.float64) @ w.astype(np.float64).T + b
+    dx, dw, db, dpos = (ctx.upload_new(a) for a in (x, w, b, pos))
+    # GELU -> fp16
+    dy = ctx.alloc(m * n * 2)
+    L.check(L.lib().mz_linear(ctx.h, linear_args(epilogue=L.EPI_GELU_F16, a=dx, lda=k, w=dw, bias=db, m=m, n=n, k=k,
+                                                 out=dy, ldo=n)))
+    assert_f16(ctx.download(dy, (m, n), np.float16), R.gelu(acc.astype(np.float32)))
+    # residual add into fp32
+    dr = ctx.upload_new(res)
+    L.check(L.lib().mz_linear(ctx.h, linear_args(epilogue=L.EPI_RESID_F32, a=dx, lda=k, w=dw, bias=db, m=m, n=n, k=k,
+                                                 out=dr, ldo=n)))
+    got = ctx.download(dr, (m, n), np.float32)
+    ref = res + acc
+    assert rel_err(got, ref) < 1e-5
+    # GELU + positions (the conv2 epilogue) exists only on the implicit-conv load: refused on a plain product
+    with pytest.raises(L.MzError):
+        L.check(L.lib().mz_linear(ctx.h, linear_args(epilogue=L.EPI_GELU_POS, a=dx, lda=k, w=dw, bias=db, m=m, n=n,
+                                                     k=k, out=dr, ldo=n, pos=dpos)))
+    for p in (dx, dw, db, dpos, dy, dr):
+        ctx.free(p)
+
+
+@pytest.mark.parametrize("kind", [3, 2])
+def test_gemm_head_scatter(ctx, kind):
+    """kind 3: [q|k|v][head] tiles of the encoder self-attention (v tiles transposed); kind 2: [layer][k|v][head] of
+    the cross k/v (all tiles row-major); both into clip slots (slot0 offset)."""
+    rng = np.random.default_rng(kind)
+    nh, clips, slot0 = 2, 2, 1
+    groups = 3 if kind == 3 else 2 * 2  # kind 2: two decoder layers
+    n, k, m = groups * nh * 64, 128, clips * 1500
+    x, w, b = f16(rng, (m, k)), f16(rng, (n, k), 0.1), f16(rng, (n,), 0.1)
+    dx, dw, db = (ctx.upload_new(a) for a in (x, w, b))
+    bpc = groups * nh
+    nslots = slot0 + clips
+    dh = ctx.alloc(nslots * bpc * TPAD * 64 * 2)
+    L.check(L.lib().mz_linear(ctx.h, linear_args(epilogue=L.EPI_HEADS, a=dx, lda=k, w=dw, bias=db, m=m, n=n, k=k,
+                                                 heads=dh, blocks_per_clip=bpc, nh=nh, kind=kind, slot0=slot0)))
+    got = ctx.download(dh, (nslots, bpc, TPAD * 64), np.float16)
+    ref = (x.astype(np.float64) @ w.astype(np.float64).T + b).reshape(clips, 1500, bpc, 64)
+    assert not got[:slot0].any(), "a slot before slot0 was written"
+    for c in range(clips):
+        for blk in range(bpc):
+            tile = got[slot0 + c, blk]
+            if kind == 3 and blk // nh == 2:  # encoder v: [64][1536]
+                t = tile.reshape(64, TPAD)
+                assert not t[:, 1500:].any()
+                assert_f16(t[:, :1500].T, ref[c, :, blk])
+            else:
+                t = tile.reshape(TPAD, 64)
+                assert not t[1500:].any()
+                assert_f16(t[:1500], ref[c, :, blk])
+    for p in (dx, dw, db, dh):
+        ctx.free(p)
+
+
+def test_gemm_large_qkv_shape(ctx):
+    """The encoder group's fused QKV product, M = 12000, N = 3840, K = 1280, 256 rows checked."""
+    rng = np.random.default_rng(5)
+    m, n, k = 12000, 3840, 1280
+    x, w, b = f16(rng, (m, k)), f16(rng, (n, k), 0.02), f16(rng, (n,), 0.02)
+    dx, dw, db = (ctx.upload_new(a) for a in (x, w, b))
+    dy = ctx.alloc(m * n * 2)
+    L.check(L.lib().mz_gemm(ctx.h, dx, k, dw, dy, n, m, n, k, db))
+    y = ctx.download(dy, (m, n), np.float16)
+    rows = np.r_[rng.choice(m, 250, replace=False), m - 6:m]
+    ref = x[rows].astype(np.float64) @ w.astype(np.float64).T + b
+    assert_f16(y[rows], ref)
+    for p in (dx, dw, db, dy):
+        ctx.free(p)
+
+
+def test_conv_stem_implicit_gemm(ctx):
+    """mel transpose + conv1 (k 3, pad 1) + GELU, conv2 (stride 2) + GELU + positions, against the oracle's conv1d."""
+    rng = np.random.default_rng(6)
+    nm, d, clips = 80, 384, 2
+    mel = np.clip(rng.normal(-0.3, 0.4, (clips, nm, 3000)), -1.5, 1.5).astype(np.float32)
+    w1, b1 = f16(rng, (d, nm, 3), 0.05), f16(rng, (d,), 0.05)
+    w2, b2 = f16(rng, (d, d, 3), 0.02), f16(rng, (d,), 0.05)
+    pos = f16(rng, (1500, d), 0.5)
+    k1 = ((3 * nm + 63) // 64) * 64
+    w1t = np.zeros((d, k1), np.float16)
+    w1t[:, :3 * nm] = w1.transpose(0, 2, 1).reshape(d, 3 * nm)
+    w2t = np.ascontiguousarray(w2.transpose(0, 2, 1).reshape(d, 3 * d))
+    dmel = ctx.upload_new(mel)
+    dmt = ctx.alloc(clips * 3000 * nm * 2)
+    L.check(L.lib().mz_mel_transpose(ctx.h, dmel, dmt, clips, nm))
+    mt = ctx.download(dmt, (clips, 3000, nm), np.float16)
+    np.testing.assert_array_equal(mt, mel.transpose(0, 2, 1).astype(np.float16))
+    dw1, db1, dw2, db2, dpos = (ctx.upload_new(a) for a in (w1t, b1, w2t, b2, pos))
+    dh1 = ctx.alloc(clips * 3000 * d * 2)
+    L.check(L.lib().mz_linear(ctx.h, linear_args(epilogue=L.EPI_GELU_F16, a=dmt, w=dw1, bias=db1, m=clips * 3000, n=d,
+                                                 k=k1, out=dh1, ldo=d, conv_cin=nm, conv_tin=3000, conv_tout=3000,
+                                                 conv_stride=1)))
+    h1 = ctx.download(dh1, (clips, 3000, d), np.float16)
+    dx = ctx.alloc(clips * 1500 * d * 4)
+    L.check(L.lib().mz_linear(ctx.h, linear_args(epilogue=L.EPI_GELU_POS, a=dh1, w=dw2, bias=db2, m=clips * 1500, n=d,
+                                                 k=3 * d, out=dx, ldo=d, pos=dpos, conv_cin=d, conv_tin=3000,
+                                                 conv_tout=1500, conv_stride=2)))
+    x = ctx.download(dx, (clips, 1500, d), np.float32)
+    for c in range(clips):
+        m16 = mel[c].astype(np.float16).astype(np.float64)
+        r1 = R.gelu(R.conv1d(m16, w1.astype(np.float64), b1.astype(np.float64), 1, 1).astype(np.float32))
+        assert_f16(h1[c].T, r1)
+        # conv2 on the kernel's own fp16 conv1 output (layer-local)
+        r2 = R.gelu(R.conv1d(h1[c].T.astype(np.float64), w2.astype(np.float64), b2.astype(np.float64), 2, 1)
+                    .astype(np.float32)).T + pos.astype(np.float32)
+        assert rel_err(x[c], r2) < 1e-4
+    for p in (dmel, dmt, dw1, db1, dw2, db2, dpos, dh1, dx):
+        ctx.free(p)
+
+
+# ---------------------------------------------------------------- LayerNorm
+
+@pytest.mark.parametrize("dim", [384, 1280, 2048])
+def test_layernorm_and_add_layernorm(ctx, dim):
+    rng = np.random.default_rng(dim)
+    rows = 301
+    x = (rng.standard_normal((rows, dim)) * 3 + 1).astype(np.float32)
+    dlt = f16(rng, (rows, dim))
+    w, b = f16(rng, (dim,), 0.1) + np.float16(1), f16(rng, (dim,), 0.1)
+    dxx, dd, dw, db = (ctx.upload_new(a) for a in (x, dlt, w, b))
+    dy = ctx.alloc(rows * dim * 2)
+    L.check(L.lib().mz_layernorm(ctx.h, dxx, dim, dw, db, dy, dim, rows, dim, 1e-5))
+    y = ctx.download(dy, (rows, dim), np.float16)
+    assert_f16(y, R.layer_norm(x.astype(np.float64), w, b))
+    L.check(L.lib().mz_add_layernorm(ctx.h, dxx, dd, dw, db, dy, rows, dim, 1e-5))
+    xs = ctx.download(dxx, (rows, dim), np.float32)
+    np.testing.assert_allclose(xs, x + dlt.astype(np.float32), rtol=0, atol=0)
+    y = ctx.download(dy, (rows, dim), np.float16)
+    assert_f16(y, R.layer_norm((x + dlt.astype(np.float32)).astype(np.float64), w, b))
+    for p in (dxx, dd, dw, db, dy):
+        ctx.free(p)
