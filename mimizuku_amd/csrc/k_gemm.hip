@@ -3,24 +3,30 @@
 // implicit GEMM (no im2col buffer), and the cross-attention K/V of every decoder layer. Replaces the reference's
 // cuBLAS calls with a bias prefill (src/gpu.rs:208-236, 254-286; kernels/whisper.cu:92-104, 106-139).
 //
-// Block tile BM x BN x 64 with 4 waves in a 2 x 2 grid; each wave owns a (BM/2) x (BN/2) tile of 32x32x16 MFMA
-// products. Both operands are K-contiguous, staged through LDS with an XOR swizzle of the 16-byte chunks (conflict
-// free ds_read_b128 for the operand fragments), double buffered with register prefetch of the next K tile.
-// The W tile is the MFMA A operand and the activation tile the B operand, so a lane's accumulators hold one token
-// row and 4-wide runs of output columns: epilogues store 8-byte runs, and transposed (V) stores are coalesced
-// across lanes.
+// Block tile BM x BN x 64 with 8 waves in a 2 x 4 grid (two waves per SIMD, so one wave's LDS reads overlap the
+// other's products); each wave owns a (BM/2) x (BN/4) tile of 32x32x16 MFMA products. Both operands are
+// K-contiguous and go from global memory straight into LDS (buffer_load ... lds, 16 bytes per lane, no register
+// staging), double buffered: the loads of K tile k + 1 are in flight while tile k is multiplied, with one barrier per
+// K tile. In LDS a tile row is 64 halves (128 bytes) whose 16-byte chunks are XOR-swizzled by the row index, so the
+// ds_read_b128 operand fragments are conflict free; a direct load writes lane i's 16 bytes at base + 16 i, so each
+// lane fetches the global chunk that belongs at its swizzled position. Rows past the end of an operand (and the zero
+// padding of the implicit convolution) are read through the buffer descriptor's range check, which returns zeros.
+// The activation tile is the MFMA A operand and the W tile the B operand, so lane l of a 32x32 product holds output
+// column l % 32 of eight rows: every store instruction writes two 32-column row segments. The transposed tiles of
+// the encoder's v are staged through LDS to be written as runs of token positions.
 #include "mz_common.h"
 #include "mz_kernels.h"
 
 namespace {
 
-template <int BM, int BN>
-struct Tile {
-    static constexpr int WM = BM / 2, WN = BN / 2;
-    static constexpr int TM = WM / 32, TN = WN / 32;
-    static constexpr int AL = BM * 8 / 256;  // 16-byte chunks of the A tile per thread per K tile
-    static constexpr int WL = BN * 8 / 256;
-};
+constexpr int NW = 8;  // waves per workgroup
+typedef __attribute__((address_space(3))) void lds_void;
+#define LDSP(p) ((lds_void*)(p))
+constexpr unsigned OOB = 0x80000000u;  // a buffer offset past every operand: the load returns zeros
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
 
 // Map the launch index to a tile so that the blocks one XCD receives (block i runs on XCD i % 8) form a contiguous
 // run of tiles, ordered with N fastest: concurrently resident blocks of an XCD share activation rows in its L2.
@@ -30,168 +36,200 @@ __device__ __forceinline__ int xcd_tile(int bid, int nblocks) {
 }
 
 template <int BM, int BN, int ALOAD, int EPI>
-__global__ void __launch_bounds__(256) gemm_kernel(const MzGemm p) {
-    using T = Tile<BM, BN>;
-    __shared__ __attribute__((aligned(16))) f16 sA[2][BM * 64];
-    __shared__ __attribute__((aligned(16))) f16 sW[2][BN * 64];
+__global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the buffer-resource type exists only in the device pass
+    constexpr int WM = BM / 2, WN = BN / 4, TM = WM / 32, TN = WN / 32;
+    constexpr int AR = BM / (8 * NW), WR = BN / (8 * NW);  // 8-row slices each wave loads per K tile
+    static_assert(AR >= 1 && WR >= 1 && TN >= 1, "tile too small for 8 waves");
+    __shared__ __attribute__((aligned(16))) f16 sA0[BM * 64];
+    __shared__ __attribute__((aligned(16))) f16 sA1[BM * 64];
+    __shared__ __attribute__((aligned(16))) f16 sW0[BN * 64];
+    __shared__ __attribute__((aligned(16))) f16 sW1[BN * 64];
 
     const int nbn = (p.N + BN - 1) / BN, nbm = (p.M + BM - 1) / BM;
     const int tile = xcd_tile(blockIdx.x, gridDim.x);
     if (tile >= nbm * nbn) return;
     const int bm = tile / nbn, bn = tile % nbn;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lh = lane >> 5;
+    const int wm = wave >> 2, wn = wave & 3, lr = lane & 31, lh = lane >> 5;
     const int nk = p.K >> 6;
-    const int chunk = tid & 7;
+    // this lane's slot in a direct load: row lrow of an 8-row slice, 16-byte chunk lc of the row
+    const int lrow = lane >> 3, lc = (lane & 7) ^ lrow;
 
-    // global sources of this thread's chunks
-    const f16* gW[T::WL];
+    const __amdgpu_buffer_rsrc_t rW = rsrc(p.W, (unsigned)p.N * p.K * 2);
+    unsigned voW[WR];
 #pragma unroll
-    for (int r = 0; r < T::WL; r++) {
-        int row = min(bn * BN + (tid >> 3) + 32 * r, p.N - 1);
-        gW[r] = p.W + (long)row * p.K + chunk * 8;
-    }
-    const f16* gA[T::AL];
-    int cg[T::AL], ct[T::AL];  // conv: clip and output time of the row
+    for (int r = 0; r < WR; r++) voW[r] = (unsigned)(bn * BN + wave * (BN / NW) + 8 * r + lrow) * p.K * 2 + lc * 16;
+    __amdgpu_buffer_rsrc_t rA;
+    unsigned voA[AR];
+    int srow[AR], stime[AR];  // conv: source row of tap 0 and its time index (-1 .. tin - 1), or a row past M
+    if (ALOAD == ALOAD_PLAIN) {
+        rA = rsrc(p.A, (unsigned)p.M * p.lda * 2);
 #pragma unroll
-    for (int r = 0; r < T::AL; r++) {
-        int row = min(bm * BM + (tid >> 3) + 32 * r, p.M - 1);
-        if (ALOAD == ALOAD_PLAIN) {
-            gA[r] = p.A + (long)row * p.lda + chunk * 8;
-        } else {
-            cg[r] = row / p.conv_tout;
-            ct[r] = row - cg[r] * p.conv_tout;
-            gA[r] = p.A;
+        for (int r = 0; r < AR; r++)
+            voA[r] = (unsigned)(bm * BM + wave * (BM / NW) + 8 * r + lrow) * p.lda * 2 + lc * 16;
+    } else {
+        const int clips = p.M / p.conv_tout;
+        rA = rsrc(p.A, (unsigned)clips * p.conv_tin * p.conv_cin * 2);
+#pragma unroll
+        for (int r = 0; r < AR; r++) {
+            const int m = bm * BM + wave * (BM / NW) + 8 * r + lrow;
+            const int g = m / p.conv_tout, t = m - g * p.conv_tout;
+            stime[r] = m < p.M ? p.conv_stride * t - 1 : -(1 << 20);
+            srow[r] = g * p.conv_tin + p.conv_stride * t - 1;
         }
     }
 
-    f16x8 ra[T::AL], rw[T::WL];
-    auto gload = [&](int kt) {
-#pragma unroll
-        for (int r = 0; r < T::WL; r++) rw[r] = ld8(gW[r] + kt * 64);
+    auto issue = [&](int kt, f16* a, f16* w) {
         if (ALOAD == ALOAD_PLAIN) {
 #pragma unroll
-            for (int r = 0; r < T::AL; r++) ra[r] = ld8(gA[r] + kt * 64);
+            for (int r = 0; r < AR; r++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, LDSP(a + (wave * (BM / NW) + 8 * r) * 64), 16, voA[r],
+                                                         kt * 128, 0, 0);
         } else {
-            int k0 = kt * 64 + chunk * 8;
-            int tap = k0 / p.conv_cin, ci = k0 - tap * p.conv_cin;
+            // implicit im2col: column k = tap * cin + ci of a row reads source time stride * t + tap - 1
+            const int k0 = kt * 64 + lc * 8, tap = k0 / p.conv_cin, ci = k0 - tap * p.conv_cin;
 #pragma unroll
-            for (int r = 0; r < T::AL; r++) {
-                int tt = p.conv_stride * ct[r] + tap - 1;
-                bool ok = tap < 3 && tt >= 0 && tt < p.conv_tin;
-                f16x8 z = {};
-                ra[r] = ok ? ld8(p.A + ((long)cg[r] * p.conv_tin + tt) * p.conv_cin + ci) : z;
+            for (int r = 0; r < AR; r++) {
+                const int tt = stime[r] + tap;
+                const bool ok = tap < 3 && tt >= 0 && tt < p.conv_tin;
+                const unsigned vo = ok ? (unsigned)((srow[r] + tap) * p.conv_cin + ci) * 2 : OOB;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, LDSP(a + (wave * (BM / NW) + 8 * r) * 64), 16, vo, 0, 0,
+                                                         0);
             }
         }
-    };
-    auto lstore = [&](int buf) {
 #pragma unroll
-        for (int r = 0; r < T::AL; r++) {
-            int row = (tid >> 3) + 32 * r;
-            *(f16x8*)&sA[buf][row * 64 + ((chunk ^ (row & 7)) << 3)] = ra[r];
-        }
-#pragma unroll
-        for (int r = 0; r < T::WL; r++) {
-            int row = (tid >> 3) + 32 * r;
-            *(f16x8*)&sW[buf][row * 64 + ((chunk ^ (row & 7)) << 3)] = rw[r];
-        }
+        for (int r = 0; r < WR; r++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, LDSP(w + (wave * (BN / NW) + 8 * r) * 64), 16, voW[r],
+                                                     kt * 128, 0, 0);
     };
 
-    f32x16 acc[T::TM][T::TN];
+    f32x16 acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < T::TM; i++)
+    for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < T::TN; j++) acc[i][j] = f32x16{};
-
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; kt++) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) gload(kt + 1);
+        for (int j = 0; j < TN; j++) acc[i][j] = f32x16{};
+    auto compute = [&](const f16* a, const f16* w) {
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
             const int sw = (((2 * kk + lh) ^ (lr & 7)) << 3);
-            f16x8 fa[T::TM], fw[T::TN];
+            f16x8 fa[TM], fw[TN];
 #pragma unroll
-            for (int i = 0; i < T::TM; i++) fa[i] = *(const f16x8*)&sA[buf][(wm * T::WM + i * 32 + lr) * 64 + sw];
+            for (int i = 0; i < TM; i++) fa[i] = *(const f16x8*)&a[(wm * WM + i * 32 + lr) * 64 + sw];
 #pragma unroll
-            for (int j = 0; j < T::TN; j++) fw[j] = *(const f16x8*)&sW[buf][(wn * T::WN + j * 32 + lr) * 64 + sw];
+            for (int j = 0; j < TN; j++) fw[j] = *(const f16x8*)&w[(wn * WN + j * 32 + lr) * 64 + sw];
 #pragma unroll
-            for (int i = 0; i < T::TM; i++)
+            for (int i = 0; i < TM; i++)
 #pragma unroll
-                for (int j = 0; j < T::TN; j++) acc[i][j] = mfma32(fw[j], fa[i], acc[i][j]);
+                for (int j = 0; j < TN; j++) acc[i][j] = mfma32(fa[i], fw[j], acc[i][j]);
         }
-        if (kt + 1 < nk) lstore(buf ^ 1);
+    };
+
+    // two K tiles per iteration, one per LDS buffer (distinct arrays, so the compiler sees that the loads in flight
+    // never alias the tile being read); an odd last tile is left in buffer 0
+    issue(0, sA0, sW0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+        issue(kt + 1, sA1, sW1);
+        __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the products they overlap
+        compute(sA0, sW0);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (kt + 2 < nk) issue(kt + 2, sA0, sW0);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(sA1, sW1);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     }
+    if (kt < nk) compute(sA0, sW0);
 
-    // epilogue: lane holds row m and columns n0 + {0..3} for each (i, j, q)
+    // epilogue: acc[i][j] element r is row m0 + i * 32 + 8 (r / 4) + 4 lh + r % 4, column n0 + j * 32 + lr
+    const int m0 = bm * BM + wm * WM, n0 = bn * BN + wn * WN;
+    if (EPI == EPI_HEADS) {
+        if (p.kind == 3) __syncthreads();  // every wave is done reading operands: LDS is free for the v transposes
+        const int blk = n0 >> 6;           // a wave's columns lie in one 64-wide head block (WN <= 64)
+        const bool vt = p.kind == 3 && blk / p.nh == 2;
+        if (vt) {
+            // encoder v: stage each 32-row slice of the wave's tile in LDS as [column][row] (the wave's own 32 x WN
+            // halves of sA0: 8 waves x 32 x WN <= BM x 64) and write runs of 4 token positions
+            static_assert(NW * 32 * WN <= BM * 64, "staging slice exceeds sA0");
+            f16* st = sA0 + wave * (32 * WN);
 #pragma unroll
-    for (int i = 0; i < T::TM; i++) {
-        const int m = bm * BM + wm * T::WM + i * 32 + lr;
-        if (m >= p.M) continue;
+            for (int i = 0; i < TM; i++) {
 #pragma unroll
-        for (int j = 0; j < T::TN; j++) {
+                for (int j = 0; j < TN; j++) {
+                    const float bv = p.bias ? (float)p.bias[min(n0 + j * 32 + lr, p.N - 1)] : 0.f;
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int n = bn * BN + wn * T::WN + j * 32 + 8 * q + 4 * lh;
-                if (n >= p.N) continue;
-                float v[4];
+                    for (int r = 0; r < 16; r++)
+                        st[(j * 32 + lr) * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)] = (f16)(acc[i][j][r] + bv);
+                }
+                __builtin_amdgcn_s_waitcnt(0);
+                __builtin_amdgcn_wave_barrier();
 #pragma unroll
-                for (int e = 0; e < 4; e++) v[e] = acc[i][j][4 * q + e] + (p.bias ? (float)p.bias[n + e] : 0.f);
-                if (EPI == EPI_F16) {
-                    st4((f16*)p.out + (long)m * p.ldo + n, v[0], v[1], v[2], v[3]);
-                } else if (EPI == EPI_GELU_F16) {
-                    st4((f16*)p.out + (long)m * p.ldo + n, gelu_erf(v[0]), gelu_erf(v[1]), gelu_erf(v[2]),
-                        gelu_erf(v[3]));
-                } else if (EPI == EPI_RESID_F32) {
-                    float4* o = (float4*)((float*)p.out + (long)m * p.ldo + n);
-                    float4 r = *o;
-                    r.x += v[0];
-                    r.y += v[1];
-                    r.z += v[2];
-                    r.w += v[3];
-                    *o = r;
-                } else if (EPI == EPI_GELU_POS) {
-                    const f16* ps = p.pos + (long)(m % MZ_TENC) * p.N + n;
-                    float4 r;
-                    r.x = gelu_erf(v[0]) + (float)ps[0];
-                    r.y = gelu_erf(v[1]) + (float)ps[1];
-                    r.z = gelu_erf(v[2]) + (float)ps[2];
-                    r.w = gelu_erf(v[3]) + (float)ps[3];
-                    *(float4*)((float*)p.out + (long)m * p.ldo + n) = r;
-                } else if (EPI == EPI_HEADS) {
-                    const int g = m / MZ_TENC, t = m - g * MZ_TENC;
-                    const int blk = n >> 6, dim = n & 63;
-                    f16* base = p.heads + ((long)(p.slot0 + g) * p.blocks_per_clip + blk) * (MZ_TPAD * MZ_HD);
-                    if (p.kind == 3 && blk / p.nh == 2) {  // encoder v: transposed for the P.V product
-#pragma unroll
-                        for (int e = 0; e < 4; e++) base[(long)(dim + e) * MZ_TPAD + t] = (f16)v[e];
-                    } else {
-                        st4(base + (long)t * MZ_HD + dim, v[0], v[1], v[2], v[3]);
+                for (int c = lane; c < WN * 8; c += 64) {
+                    const int nl = c >> 3, ml = (c & 7) * 4;
+                    const int m = m0 + i * 32 + ml, n = n0 + nl;
+                    if (m < p.M && n < p.N) {
+                        const int g = m / MZ_TENC, t = m - g * MZ_TENC;  // 4 | 1500: the run stays in one clip
+                        f16* dst = p.heads + ((long)(p.slot0 + g) * p.blocks_per_clip + (n >> 6)) * (MZ_TPAD * MZ_HD) +
+                                   (long)(n & 63) * MZ_TPAD + t;
+                        *(f16x4*)dst = *(const f16x4*)&st[nl * 32 + ml];
                     }
                 }
+                __builtin_amdgcn_s_waitcnt(0);
+                __builtin_amdgcn_wave_barrier();  // the slice is read before the next one overwrites it
             }
+            return;
         }
     }
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int n = n0 + j * 32 + lr;
+        if (n >= p.N) continue;
+        const float bv = p.bias ? (float)p.bias[n] : 0.f;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (m >= p.M) continue;
+                const float v = acc[i][j][r] + bv;
+                if (EPI == EPI_F16) {
+                    ((f16*)p.out)[(long)m * p.ldo + n] = (f16)v;
+                } else if (EPI == EPI_GELU_F16) {
+                    ((f16*)p.out)[(long)m * p.ldo + n] = (f16)gelu_erf(v);
+                } else if (EPI == EPI_RESID_F32) {
+                    float* o = (float*)p.out + (long)m * p.ldo + n;
+                    *o += v;
+                } else if (EPI == EPI_GELU_POS) {
+                    ((float*)p.out)[(long)m * p.ldo + n] = gelu_erf(v) + (float)p.pos[(long)(m % MZ_TENC) * p.N + n];
+                } else if (EPI == EPI_HEADS) {
+                    const int g = m / MZ_TENC, t = m - g * MZ_TENC;
+                    p.heads[((long)(p.slot0 + g) * p.blocks_per_clip + (n >> 6)) * (MZ_TPAD * MZ_HD) +
+                            (long)t * MZ_HD + (n & 63)] = (f16)v;
+                }
+            }
+    }
+#endif
 }
 
 template <int BM, int BN, int ALOAD, int EPI>
 hipError_t launch(hipStream_t s, const MzGemm& g) {
     int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
     int grid = (tiles + 7) & ~7;
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, ALOAD, EPI>), dim3(grid), dim3(256), 0, s, g);
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, ALOAD, EPI>), dim3(grid), dim3(NW * 64), 0, s, g);
     return hipGetLastError();
 }
 
 template <int ALOAD, int EPI>
 hipError_t pick(hipStream_t s, const MzGemm& g) {
-    // 256 x 256 tiles once there are enough of them to fill 256 CUs; 256 x 128 (or 128 x 128) below that
-    long t256 = (long)((g.M + 255) / 256) * ((g.N + 255) / 256);
-    if (t256 >= 512) return launch<256, 256, ALOAD, EPI>(s, g);
-    long t128 = (long)((g.M + 255) / 256) * ((g.N + 127) / 128);
-    if (t128 >= 256) return launch<256, 128, ALOAD, EPI>(s, g);
+    // 256 x 256 tiles once they cover most of the 256 CUs; 256 x 128, then 128 x 128 below that
+    const long t256 = (long)((g.M + 255) / 256) * ((g.N + 255) / 256);
+    if (t256 >= 200) return launch<256, 256, ALOAD, EPI>(s, g);
+    const long t128 = (long)((g.M + 255) / 256) * ((g.N + 127) / 128);
+    if (t128 >= 200) return launch<256, 128, ALOAD, EPI>(s, g);
     return launch<128, 128, ALOAD, EPI>(s, g);
 }
 
