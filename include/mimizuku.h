@@ -185,7 +185,7 @@ int mz_engine_profile_read(mz_engine* e, int kernel, double* total_ms, int* coun
 #define MZ_BUF_TOK 0     /* i32 [bmax][max_t] */
 #define MZ_BUF_DONE 1    /* i32 [bmax] */
 #define MZ_BUF_CTR 2     /* i32 [4]; ctr[0] = position of the next step */
-#define MZ_BUF_ALIGN 3   /* f16 [bmax][max_t][n_align][1500] alignment-head probabilities */
+#define MZ_BUF_ALIGN 3   /* f32 [bmax][max_t][n_align][1500] alignment-head probabilities */
 #define MZ_BUF_ENC_OUT 4 /* f16 [eg * 1500][d] final-LN encoder output of the last encode */
 #define MZ_BUF_LOGITS 5  /* f32 [bmax][vocab] logits of the last step */
 #define MZ_BUF_TRACE 6   /* f32 [enc_layers][eg * 1500][d] encoder layer inputs (set_trace) */
@@ -196,6 +196,7 @@ int mz_engine_profile_read(mz_engine* e, int kernel, double* total_ms, int* coun
 int mz_engine_buffer(mz_engine* e, int which, uint64_t* dptr, size_t* bytes);
 /* Synchronise, then copy bytes at byte offset `offset` of an engine buffer to host memory. */
 int mz_engine_read(mz_engine* e, int which, void* dst, size_t offset, size_t bytes);
+/* Frees the engine's device and host memory; call it before mz_ctx_free of its context. */
 int mz_engine_free(mz_engine* e);
 
 /* Wall times of the stages, seconds (Times, src/transcribe.rs:95-101). */

@@ -124,7 +124,6 @@ namespace {
 // network vectorises over frames.
 inline float rhw(float x) { return _cvtsh_ss(_cvtss_sh(x, 0)); }
 inline float load_w(const float* w, size_t i) { return w[i]; }
-inline float load_w(const uint16_t* w, size_t i) { return _cvtsh_ss(w[i]); }
 
 inline void cswap(float& a, float& b) {
     const float lo = a < b ? a : b, hi = a < b ? b : a;
@@ -144,7 +143,7 @@ inline float median7(const float* p) {
     return a[3];
 }
 
-// Token start times (src/align.rs:8-63) from w [rows][heads][cols_full] (f32 or fp16 bits).
+// Token start times (src/align.rs:8-63) from w [rows][heads][cols_full].
 template <class T>
 void jump_times_impl(const T* w, int rows, int heads, int cols_full, int cols, int width, int half, float* out) {
     if (rows == 0) return;
@@ -242,15 +241,6 @@ static int host_ok() {
 
 extern "C" int mz_jump_times(const float* w, int rows, int heads, int cols_full, int cols, int width, int half,
                              float* out) {
-    if (!w || !out || !jump_args_ok(rows, heads, cols_full, cols, width))
-        return mz_fail(MZ_ERR_ARG, "mz_jump_times: bad argument");
-    if (int r = host_ok()) return r;
-    jump_times_impl(w, rows, heads, cols_full, cols, width, half, out);
-    return MZ_OK;
-}
-
-int mz_jump_times_f16(const uint16_t* w, int rows, int heads, int cols_full, int cols, int width, int half,
-                      float* out) {
     if (!w || !out || !jump_args_ok(rows, heads, cols_full, cols, width))
         return mz_fail(MZ_ERR_ARG, "mz_jump_times: bad argument");
     if (int r = host_ok()) return r;

@@ -83,8 +83,9 @@ struct mz_engine {
     f16* xkvbuf = nullptr;
     int *tok = nullptr, *done = nullptr, *ctr = nullptr;
     float *x = nullptr, *q = nullptr, *part = nullptr, *logits = nullptr;
-    f16 *h = nullptr, *datt = nullptr, *dff = nullptr, *kc = nullptr, *vc = nullptr, *align = nullptr;
-    int2* amax = nullptr;  // LM head argmax partials [ceil(vocab / 32)][bmax]
+    f16 *h = nullptr, *datt = nullptr, *dff = nullptr, *kc = nullptr, *vc = nullptr;
+    float* align = nullptr;  // alignment-head probabilities [bmax][max_t][na][1500], fp32
+    int2* amax = nullptr;  // LM head argmax partials [ceil(vocab / MZ_LM_COLS)][bmax]
     int* aslot = nullptr;
     unsigned char *sup = nullptr, *sup_lang = nullptr;
     size_t part_elems = 0;
@@ -109,7 +110,7 @@ struct mz_engine {
         return x;
     }
     // pinned host staging of the alignment rows read back after decoding (hipHostMalloc'd on first use)
-    uint16_t* align_host = nullptr;
+    float* align_host = nullptr;
     size_t align_host_bytes = 0;
     // position of the next step as the host has enqueued it (the device copy is ctr[0]); steps beyond the cache
     // (max_t - 1 of them after a reset) are refused
@@ -166,7 +167,7 @@ extern "C" size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int 
     size_t enc = G * d->n_mels * NFR * 4 + G * NFR * d->n_mels * 2 + G * NFR * D * 2 + G * TENC * D * 4 +
                  G * TENC * D * 2 * 2 + G * 3 * nh * TPAD * HD * 2 + G * TENC * F * 2;
     size_t dec = B * nl * 2 * nh * TPAD * HD * 2 + B * mt * 4 + B * 4 + 16 + B * D * 4 * 2 + B * D * 2 * 2 + B * F * 2 +
-                 2 * nl * B * nh * mt * HD * 2 + B * V * 4 + B * mt * n_align * TENC * 2 + (V + 31) / 32 * B * 8 +
+                 2 * nl * B * nh * mt * HD * 2 + B * V * 4 + B * mt * n_align * TENC * 4 + (V + MZ_LM_COLS - 1) / MZ_LM_COLS * B * 8 +
                  nl * nh * 4 + 2 * V;
     size_t part = (size_t)MZ_MAX_PARTS * B * D * 4;
     return enc + dec + part;
@@ -310,7 +311,7 @@ extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, in
         (r = e->alloc(&e->dff, B * F)) || (r = e->alloc(&e->kc, (size_t)nl * B * nh * mt * HD)) ||
         (r = e->alloc(&e->vc, (size_t)nl * B * nh * mt * HD)) || (r = e->alloc(&e->logits, B * V)) ||
         (r = e->alloc(&e->align, B * mt * e->na * (size_t)TENC)) ||
-        (r = e->alloc(&e->amax, (size_t)((V + 31) / 32) * B)) ||
+        (r = e->alloc(&e->amax, (size_t)((V + MZ_LM_COLS - 1) / MZ_LM_COLS) * B)) ||
         (r = e->alloc(&e->aslot, (size_t)nl * nh)) || (r = e->alloc(&e->sup, V)) || (r = e->alloc(&e->sup_lang, V)))
         return fail(r);
     // split-K partials: the largest ks * rows * n over the decoder products
@@ -698,7 +699,7 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
         g.amax = e->amax;
         TRY(mz_dec_gemm_launch(s, DEPI_LOGITS, g), "lm head");
     }
-    TRY(mz_dec_argmax_launch(s, e->amax, (V + 31) / 32, e->tok, e->done, e->ctr, b, mt, prompt_len, e->eos), "argmax");
+    TRY(mz_dec_argmax_launch(s, e->amax, (V + MZ_LM_COLS - 1) / MZ_LM_COLS, e->tok, e->done, e->ctr, b, mt, prompt_len, e->eos), "argmax");
     return MZ_OK;
 }
 
@@ -763,7 +764,7 @@ extern "C" int mz_engine_buffer(mz_engine* e, int which, uint64_t* dptr, size_t*
         case MZ_BUF_TOK: p = e->tok, n = B * mt * 4; break;
         case MZ_BUF_DONE: p = e->done, n = B * 4; break;
         case MZ_BUF_CTR: p = e->ctr, n = 16; break;
-        case MZ_BUF_ALIGN: p = e->align, n = B * mt * e->na * TENC * 2; break;
+        case MZ_BUF_ALIGN: p = e->align, n = B * mt * e->na * TENC * 4; break;
         case MZ_BUF_ENC_OUT: p = e->hb, n = G * TENC * D * 2; break;
         case MZ_BUF_LOGITS: p = e->logits, n = B * e->dm.vocab * 4; break;
         case MZ_BUF_TRACE:
@@ -883,18 +884,18 @@ static int transcribe_impl(mz_engine* e, const float* mels, bool on_device, cons
         nrows[c] = std::max(n_seq - 1 - np, 0);
         off[c + 1] = off[c] + (size_t)nrows[c] * row;
     }
-    if (off[n] * 2 > e->align_host_bytes) {
+    if (off[n] * 4 > e->align_host_bytes) {
         if (e->align_host) hipHostFree(e->align_host);
         e->align_host = nullptr;
         e->align_host_bytes = 0;
-        const size_t want = (size_t)e->bmax * mt * row * 2;
+        const size_t want = (size_t)e->bmax * mt * row * 4;
         TRY(hipHostMalloc((void**)&e->align_host, want, hipHostMallocDefault), "hipHostMalloc");
         e->align_host_bytes = want;
     }
     for (int c = 0; c < n; c++)
         if (nrows[c] > 0)
             TRY(hipMemcpyAsync(e->align_host + off[c], e->align + ((size_t)c * mt + np) * row,
-                               (size_t)nrows[c] * row * 2, hipMemcpyDeviceToHost, e->c->stream),
+                               (size_t)nrows[c] * row * 4, hipMemcpyDeviceToHost, e->c->stream),
                 "align download");
     if (int r = mz_sync(e->c)) return r;
     // token timestamps per clip (median filter + DTW on the host), clips in parallel
@@ -905,7 +906,7 @@ static int transcribe_impl(mz_engine* e, const float* mels, bool on_device, cons
         for (int c; (c = next.fetch_add(1)) < n;) {
             if (nrows[c] <= 0) continue;
             jts[c].resize(nrows[c]);
-            rcs[c] = mz_jump_times_f16(e->align_host + off[c], nrows[c], e->na, TENC, frames[c] / 2, 7, half_align,
+            rcs[c] = mz_jump_times(e->align_host + off[c], nrows[c], e->na, TENC, frames[c] / 2, 7, half_align,
                                        jts[c].data());
         }
     };

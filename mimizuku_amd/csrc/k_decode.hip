@@ -12,7 +12,7 @@
 //   dec_embed_ln  token + position embedding fused with the first LayerNorm (whisper.cu:303-307, 65-69)
 //   dec_gemm      skinny GEMM for M <= 32 rows per tile on the matrix cores: W rows are the 32x32x16 MFMA A
 //                 operand, x rows the B operand; split-K over workgroups (grid.y) and over the 4 waves of a
-//                 workgroup, every wave issuing its loads 4 groups of 64 columns at a time. Epilogues: fp32
+//                 workgroup, every wave issuing all its loads at once (the LM head two column tiles). Epilogues: fp32
 //                 split-K partials, GELU -> fp16, fp16, the self-attention q/k/v scatter into the cache, or logits
 //                 with a masked per-workgroup argmax (gemv_* + cuBLAS + fill_bias + kv_write, whisper.cu:92-97,
 //                 309-317, 497-567)
@@ -26,8 +26,6 @@
 
 namespace {
 
-constexpr int AG = 64;  // groups of 8 lanes per attention workgroup (512 threads)
-constexpr int AU = 4;   // keys in flight per group
 
 // sum over a workgroup whose size is a multiple of 64 (at most 1024); red holds 16 floats
 __device__ __forceinline__ float block_sum(float v, float* red) {
@@ -115,61 +113,84 @@ __global__ void __launch_bounds__(512) dec_embed_ln_kernel(const int* __restrict
 
 // ---------------------------------------------------------------- skinny GEMM
 
-template <int EPI>
+// NT column tiles of 32 per wave (the LM head uses 2, so each x fragment feeds two products: the x rows, read by
+// every workgroup, are half of the traffic otherwise); DG groups of 64 columns in flight per wave. Every operand of
+// the epilogue (bias, mask, position) is requested at entry, so the kernel makes a single round trip to memory.
+template <int EPI, int NT>
 __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
-    __shared__ float red[4][32][33];
+    constexpr int DG = NT == 1 ? 5 : 3;
+    constexpr int NC = 4 * NT;  // output columns per epilogue thread
+    __shared__ float red[4][32 * NT][33];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, lh = lane >> 5;
-    const int n0 = blockIdx.x * 32, ks = blockIdx.y, m0 = blockIdx.z * 32;
+    const int n0 = blockIdx.x * 32 * NT, ks = blockIdx.y, m0 = blockIdx.z * 32;
     const int gpb = (p.K >> 6) / p.ksplit, gbeg = ks * gpb;
+    const int ml = tid >> 3, nl = (tid & 7) * NC, m = m0 + ml;
 
-    const f16* wr = p.W + (long)min(n0 + lr, p.N - 1) * p.K + lh * 32;
-    const f16* xr = p.x + (long)min(m0 + lr, p.M - 1) * p.ldx + lh * 32;
-    f32x16 acc = {};
-    // wave w takes groups w, w + 4, w + 8, ... of the workgroup's K range, four of them in flight at a time
-    for (int g0 = wave; g0 < gpb; g0 += 16) {
-        f16x8 wv[4][4], xv[4][4];
+    // epilogue operands first
+    float bv[NC];
+    bool msk[NC];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+    for (int e = 0; e < NC; e++) {
+        const int n = min(n0 + nl + e, p.N - 1);
+        bv[e] = (EPI != DEPI_PARTIAL && p.bias) ? (float)p.bias[n] : 0.f;
+        msk[e] = EPI == DEPI_LOGITS ? p.sup[n] != 0 : false;
+    }
+    const int pos = (EPI == DEPI_LOGITS || EPI == DEPI_QKV) ? p.ctr[1] : 0;
+
+    const f16* wr[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) wr[t] = p.W + (long)min(n0 + 32 * t + lr, p.N - 1) * p.K + lh * 32;
+    const f16* xr = p.x + (long)min(m0 + lr, p.M - 1) * p.ldx + lh * 32;
+    f32x16 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = f32x16{};
+    // wave w takes groups w, w + 4, w + 8, ... of the workgroup's K range, DG of them in flight at a time
+    for (int g0 = wave; g0 < gpb; g0 += 4 * DG) {
+        f16x8 wv[DG][NT][4], xv[DG][4];
+#pragma unroll
+        for (int i = 0; i < DG; i++) {
             const int gi = g0 + 4 * i;
             if (gi < gpb) {
                 const int k0 = (gbeg + gi) * 64;
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
-                    wv[i][c] = ld8(wr + k0 + 8 * c);
+#pragma unroll
+                    for (int t = 0; t < NT; t++) wv[i][t][c] = ld8(wr[t] + k0 + 8 * c);
                     xv[i][c] = ld8(xr + k0 + 8 * c);
                 }
             }
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < DG; i++)
             if (g0 + 4 * i < gpb) {
 #pragma unroll
-                for (int c = 0; c < 4; c++) acc = mfma32(wv[i][c], xv[i][c], acc);
+                for (int c = 0; c < 4; c++)
+#pragma unroll
+                    for (int t = 0; t < NT; t++) acc[t] = mfma32(wv[i][t][c], xv[i][c], acc[t]);
             }
     }
-    // accumulator r: n = n0 + 8 (r / 4) + 4 lh + r % 4, m = m0 + lr
+    // accumulator r of tile t: n = n0 + 32 t + 8 (r / 4) + 4 lh + r % 4, m = m0 + lr
 #pragma unroll
-    for (int r = 0; r < 16; r++) red[wave][8 * (r >> 2) + 4 * lh + (r & 3)][lr] = acc[r];
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) red[wave][32 * t + 8 * (r >> 2) + 4 * lh + (r & 3)][lr] = acc[t][r];
     __syncthreads();
-    const int ml = tid >> 3, nl = (tid & 7) * 4;
-    const int m = m0 + ml;
-    float v[4];
+    float v[NC];
 #pragma unroll
-    for (int e = 0; e < 4; e++)
+    for (int e = 0; e < NC; e++)
         v[e] = red[0][nl + e][ml] + red[1][nl + e][ml] + red[2][nl + e][ml] + red[3][nl + e][ml];
 
     if (EPI == DEPI_LOGITS) {
-        // logits, and the largest unmasked one of this workgroup's 32 columns per row (lowest id on ties)
-        const int pos = p.ctr[1];
+        // logits, and the largest unmasked one of this workgroup's columns per row (lowest id on ties)
         const bool first = pos + 1 == p.prompt_len;
         float best = -INFINITY;
         int bi = 0x7fffffff;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
+        for (int e = 0; e < NC; e++) {
             const int n = n0 + nl + e;
             if (m < p.M && n < p.N) {
                 ((float*)p.out)[(long)m * p.ldo + n] = v[e];
-                const bool masked = p.sup[n] || (first && (n == p.bs1 || n == p.bs2));
+                const bool masked = msk[e] || (first && (n == p.bs1 || n == p.bs2));
                 if (!masked && (v[e] > best || (v[e] == best && n < bi))) {
                     best = v[e];
                     bi = n;
@@ -194,17 +215,15 @@ __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
         return;
     }
     if (m >= p.M) return;
-    const int pos = EPI == DEPI_QKV ? p.ctr[1] : 0;
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
+    for (int e = 0; e < NC; e++) {
         const int n = n0 + nl + e;
         if (n >= p.N) continue;
-        float a = v[e];
         if (EPI == DEPI_PARTIAL) {
-            ((float*)p.out)[((long)ks * p.M + m) * p.ldo + n] = a;
+            ((float*)p.out)[((long)ks * p.M + m) * p.ldo + n] = v[e];
             continue;
         }
-        if (p.bias) a += (float)p.bias[n];
+        const float a = v[e] + bv[e];
         if (EPI == DEPI_GELU_F16) {
             ((f16*)p.out)[(long)m * p.ldo + n] = (f16)gelu_erf(a);
         } else if (EPI == DEPI_F16) {
@@ -224,11 +243,15 @@ __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
 
 // ---------------------------------------------------------------- attention of one query per (row, head)
 
-// One workgroup per (row, head): 64 groups of 8 lanes stream the keys round-robin (a lane holds 8 of the 64 dims),
+// One workgroup per (row, head): AG groups of 8 lanes stream the keys round-robin (a lane holds 8 of the 64 dims),
 // loading each key's k and v rows together, and keep a private online softmax; the groups merge in LDS. Scores are
 // in the log2 domain (log2(e) / 8 folded into q), all arithmetic fp32. The alignment heads' probabilities are
 // written for position ctr[1] from the scores kept in LDS.
-__global__ void __launch_bounds__(512) dec_attn_kernel(const MzDecAttn a) {
+// AG groups of 8 lanes per workgroup, AU keys in flight per group: the cross-attention uses 32 x 8 (every (row, head)
+// workgroup of a 32-row batch resident at once, 64 KB in flight each), the self-attention over at most 448 cached
+// positions 64 x 4 (one pass over a 200-position cache).
+template <int AG, int AU>
+__global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
     __shared__ float qs[MZ_HD];
     __shared__ float sc[MZ_TPAD];
     __shared__ float gm[AG], gl[AG];
@@ -242,6 +265,19 @@ __global__ void __launch_bounds__(512) dec_attn_kernel(const MzDecAttn a) {
     const int L = a.L > 0 ? a.L : min(pos + 1, a.maxT);
     const int slot = a.aslot ? a.aslot[head] : -1;
 
+    // the first batch of keys and values is requested before the query, which arrives in the same round trip
+    const f16* kb = a.k + (long)b * a.kv_b + (long)head * a.kv_h + sub * 8;
+    const f16* vb = a.v + (long)b * a.kv_b + (long)head * a.kv_h + sub * 8;
+    f16x8 kk[AU], vv[AU];
+    auto fetch = [&](int j0) {
+#pragma unroll
+        for (int u = 0; u < AU; u++) {
+            const int j = j0 + u * AG;
+            kk[u] = j < L ? ld8(kb + (long)j * MZ_HD) : f16x8{};
+            vv[u] = j < L ? ld8(vb + (long)j * MZ_HD) : f16x8{};
+        }
+    };
+    fetch(grp);
     if (tid < MZ_HD) {
         float q = a.qbias ? (float)a.qbias[head * MZ_HD + tid] : 0.f;
         for (int s = 0; s < a.nq; s++) q += a.q[s * a.qstride + (long)b * a.d + head * MZ_HD + tid];
@@ -252,17 +288,9 @@ __global__ void __launch_bounds__(512) dec_attn_kernel(const MzDecAttn a) {
 #pragma unroll
     for (int e = 0; e < 8; e++) q8[e] = qs[sub * 8 + e];
 
-    const f16* kb = a.k + (long)b * a.kv_b + (long)head * a.kv_h + sub * 8;
-    const f16* vb = a.v + (long)b * a.kv_b + (long)head * a.kv_h + sub * 8;
     float m = -INFINITY, l = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int j0 = grp; j0 < L; j0 += AG * AU) {
-        f16x8 kk[AU], vv[AU];
-#pragma unroll
-        for (int u = 0; u < AU; u++) {
-            const int j = j0 + u * AG;
-            kk[u] = j < L ? ld8(kb + (long)j * MZ_HD) : f16x8{};
-            vv[u] = j < L ? ld8(vb + (long)j * MZ_HD) : f16x8{};
-        }
+        if (j0 != grp) fetch(j0);
         float s[AU];
 #pragma unroll
         for (int u = 0; u < AU; u++) {
@@ -318,8 +346,8 @@ __global__ void __launch_bounds__(512) dec_attn_kernel(const MzDecAttn a) {
     if (slot < 0 || pos >= a.maxT) return;
     __syncthreads();
     const float M = tot[0], inv = 1.f / tot[1];
-    f16* al = a.align + (((long)b * a.maxT + pos) * a.na + slot) * MZ_TENC;
-    for (int j = tid; j < L; j += blockDim.x) al[j] = (f16)(__builtin_amdgcn_exp2f(sc[j] - M) * inv);
+    float* al = a.align + (((long)b * a.maxT + pos) * a.na + slot) * MZ_TENC;
+    for (int j = tid; j < L; j += blockDim.x) al[j] = __builtin_amdgcn_exp2f(sc[j] - M) * inv;
 }
 
 // ---------------------------------------------------------------- greedy choice
@@ -389,11 +417,15 @@ hipError_t mz_dec_gemm_launch(hipStream_t s, int epi, const MzDec& g) {
     if (epi != DEPI_PARTIAL && g.ksplit != 1) return hipErrorInvalidValue;
     dim3 grid((g.N + 31) / 32, g.ksplit, (g.M + 31) / 32);
     switch (epi) {
-        case DEPI_PARTIAL: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_PARTIAL>, grid, dim3(256), 0, s, g); break;
-        case DEPI_GELU_F16: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_GELU_F16>, grid, dim3(256), 0, s, g); break;
-        case DEPI_QKV: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_QKV>, grid, dim3(256), 0, s, g); break;
-        case DEPI_F16: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_F16>, grid, dim3(256), 0, s, g); break;
-        case DEPI_LOGITS: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_LOGITS>, grid, dim3(256), 0, s, g); break;
+        case DEPI_PARTIAL: hipLaunchKernelGGL((dec_gemm_kernel<DEPI_PARTIAL, 1>), grid, dim3(256), 0, s, g); break;
+        case DEPI_GELU_F16: hipLaunchKernelGGL((dec_gemm_kernel<DEPI_GELU_F16, 1>), grid, dim3(256), 0, s, g); break;
+        case DEPI_QKV: hipLaunchKernelGGL((dec_gemm_kernel<DEPI_QKV, 1>), grid, dim3(256), 0, s, g); break;
+        case DEPI_F16: hipLaunchKernelGGL((dec_gemm_kernel<DEPI_F16, 1>), grid, dim3(256), 0, s, g); break;
+        case DEPI_LOGITS:
+            grid.x = (g.N + MZ_LM_COLS - 1) / MZ_LM_COLS;
+            static_assert(MZ_LM_COLS == 64, "two 32-column tiles per workgroup");
+            hipLaunchKernelGGL((dec_gemm_kernel<DEPI_LOGITS, 2>), grid, dim3(256), 0, s, g);
+            break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -402,7 +434,10 @@ hipError_t mz_dec_gemm_launch(hipStream_t s, int epi, const MzDec& g) {
 hipError_t mz_dec_attn_launch(hipStream_t s, const MzDecAttn& a) {
     if (a.maxT <= 0 || a.B <= 0 || a.nh <= 0 || a.L > MZ_TPAD || (a.L <= 0 && a.maxT > MZ_TPAD)) return hipErrorInvalidValue;
     if (a.aslot && (!a.align || a.na <= 0 || (a.L > 0 && a.L != MZ_TENC))) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(dec_attn_kernel, dim3(a.B * a.nh), dim3(AG * 8), 0, s, a);
+    if (a.L > 0)
+        hipLaunchKernelGGL((dec_attn_kernel<32, 8>), dim3(a.B * a.nh), dim3(32 * 8), 0, s, a);
+    else
+        hipLaunchKernelGGL((dec_attn_kernel<64, 4>), dim3(a.B * a.nh), dim3(64 * 8), 0, s, a);
     return hipGetLastError();
 }
 

@@ -25,7 +25,3 @@ int mz_ctx_alloc(mz_ctx* c, size_t bytes, void** p);
 // IEEE binary16 conversions (round to nearest even), host side
 uint16_t mz_f2h_host(float x);
 float mz_h2f_host(uint16_t h);
-
-// token start times from alignment-head weights held as fp16 bits (the engine's align rows), as mz_jump_times
-int mz_jump_times_f16(const uint16_t* w, int rows, int heads, int cols_full, int cols, int width, int half,
-                      float* out);

@@ -57,6 +57,7 @@ hipError_t mz_mel_transpose_launch(hipStream_t s, const float* mel, f16* melT, i
 // Position: ctr[0] = position of the next step; the step's first kernel (embed) copies it to ctr[1], the later
 // kernels read ctr[1], the last one (argmax) writes ctr[0] = ctr[1] + 1.
 #define MZ_MAX_PARTS 16  // split-K partials summed by dec_add_ln
+#define MZ_LM_COLS 64    // LM head columns per workgroup: one argmax partial per 64 vocabulary ids and row
 
 // skinny GEMM for decode batches: rows m < M of x (f16, row stride ldx, M <= 32 per m-tile) times W[N][K]
 enum MzDecEpi {
@@ -82,7 +83,7 @@ struct MzDec {
     // DEPI_LOGITS: mask (nonzero = never chosen), begin-suppressed ids at the first generated position, partials
     const unsigned char* sup;
     int bs1, bs2, prompt_len;
-    void* amax;  // int2 {float bits, id} [grid.x][M]
+    void* amax;  // int2 {float bits, id} [ceil(N / MZ_LM_COLS)][M]
 };
 hipError_t mz_dec_gemm_launch(hipStream_t s, int epi, const MzDec& g);
 
@@ -104,7 +105,7 @@ struct MzDecAttn {
     int maxT;
     // alignment-head capture (cross only, may be null): slot of each head of this layer or -1
     const int* aslot;
-    f16* align;        // [bmax][maxT][na][1500]
+    float* align;      // [bmax][maxT][na][1500]
     int na;
 };
 hipError_t mz_dec_attn_launch(hipStream_t s, const MzDecAttn& a);

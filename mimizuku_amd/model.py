@@ -11,6 +11,7 @@ import ctypes as C
 import dataclasses
 import json
 import os
+import weakref
 
 import numpy as np
 
@@ -22,14 +23,17 @@ NFRAMES = 3000
 
 
 class Context:
-    """One device and its stream (the reference's `Gpu`)."""
+    """One device and its stream (the reference's `Gpu`). Closing it first closes the engines built on it."""
 
     def __init__(self, device: int = 0):
         self.h = C.c_void_p()
+        self.engines = weakref.WeakSet()
         check(L.lib().mz_init(device, C.byref(self.h)))
 
     def close(self):
         if self.h:
+            for e in list(self.engines):
+                e.close()
             L.lib().mz_ctx_free(self.h)
             self.h = C.c_void_p()
 
@@ -198,6 +202,7 @@ class Engine:
         gcs, keep = gc.c()
         check(L.lib().mz_engine_new(ctx.h, C.byref(dc), C.byref(gcs), bmax, eg, C.byref(self.h)))
         del keep
+        ctx.engines.add(self)
 
     @staticmethod
     def new(model_dir: str, bmax: int, eg: int, ctx: Context | None = None) -> "Engine":
@@ -228,7 +233,8 @@ class Engine:
 
     def close(self):
         if self.h:
-            L.lib().mz_engine_free(self.h)
+            if self.ctx.h:  # the context frees its engines' device memory itself when it is closed first
+                L.lib().mz_engine_free(self.h)
             self.h = C.c_void_p()
 
     def __del__(self):
@@ -306,8 +312,8 @@ class Engine:
         return self.read(L.BUF_LOGITS, np.float32, (self.bmax, self.dims.vocab))
 
     def align(self) -> np.ndarray:
-        """[bmax][max_t][n_align][1500] alignment-head probabilities (fp16)."""
-        return self.read(L.BUF_ALIGN, np.float16, (self.bmax, self.dims.max_t, len(self.gc.align_heads), TENC))
+        """[bmax][max_t][n_align][1500] alignment-head probabilities (fp32)."""
+        return self.read(L.BUF_ALIGN, np.float32, (self.bmax, self.dims.max_t, len(self.gc.align_heads), TENC))
 
     def enc_out(self, n: int | None = None) -> np.ndarray:
         n = n or self.eg
