@@ -43,7 +43,7 @@ def kernel_work(g, G: int) -> dict:
         "mel": ("hbm", G * nm * 3000 * (4 + 2)),
         "conv1": ("mfma", 2.0 * G * 3000 * d * 3 * nm),
         "conv2": ("mfma", 2.0 * M * d * 3 * d),
-        "ln": ("hbm", M * d * (4 + 2)),
+        "ln": ("hbm", M * d * (4 + 2 + 4 + 2)),  # add + LayerNorm: read x (f32) and the fp16 delta, write x and h
         "qkv": ("mfma", 2.0 * M * 3 * d * d),
         "attn": ("mfma", 4.0 * G * nh * 1500 * 1500 * 64),
         "oproj": ("mfma", 2.0 * M * d * d),
@@ -114,6 +114,69 @@ def cpu_baseline(g, W16: dict, gen: dict, mel: np.ndarray, steps: int) -> dict:
                        f"{steps} steps = {total:.1f}s")}
 
 
+def probe(name: str, reps: int = 5):
+    """Runs one encoder kernel class at the bench's shape (8 clips x 1500 frames, large-v3-turbo widths), or a plain
+    device-to-device copy of known size, for counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)."""
+    import ctypes as C
+    from mimizuku_amd import _lib as L, model, synth
+    g = synth.LARGE_V3_TURBO
+    d, ff, nh = g.d, g.ff, g.nh
+    M = EG * 1500
+    ctx = model.Context(0)
+    rng = np.random.default_rng(0)
+
+    def f16(shape, sc=1.0):
+        return (rng.standard_normal(shape, dtype=np.float32) * sc).astype(np.float16)
+
+    if name == "copy":
+        nbytes = 512 << 20
+        a, b = ctx.alloc(nbytes), ctx.alloc(nbytes)
+        for _ in range(reps):
+            L.check(L.lib().mz_copy(ctx.h, b, a, nbytes))
+        ctx.sync()
+        print(json.dumps({"probe": "copy", "bytes_read": nbytes, "bytes_written": nbytes, "launches": reps}))
+        return
+    la = L.LinearArgs()
+    x = ctx.upload_new(f16((M, ff)))
+    w = ctx.upload_new(f16((g.dec_layers * 2 * d, 3 * d), 0.02))
+    bias = ctx.upload_new(f16((g.dec_layers * 2 * d,), 0.02))
+    out = ctx.alloc(M * max(ff, g.dec_layers * 2 * d) * 4)
+    heads = ctx.alloc(EG * max(3, 2 * g.dec_layers) * nh * 1536 * 64 * 2)
+    pos = ctx.upload_new(f16((1500, d)))
+    for k, v in dict(a=x, lda=d, w=w, bias=bias, m=M, n=d, k=d, out=out, ldo=d).items():
+        setattr(la, k, v)
+    if name == "qkv":
+        la.epilogue, la.n, la.heads, la.blocks_per_clip, la.nh, la.kind = L.EPI_HEADS, 3 * d, heads, 3 * nh, nh, 3
+    elif name == "oproj":
+        la.epilogue = L.EPI_F16
+    elif name == "fc1":
+        la.epilogue, la.n, la.ldo = L.EPI_GELU_F16, ff, ff
+    elif name == "fc2":
+        la.epilogue, la.k, la.lda = L.EPI_F16, ff, ff
+    elif name == "conv1":
+        la.epilogue, la.m, la.k = L.EPI_GELU_F16, EG * 3000, ((3 * g.n_mels + 63) // 64) * 64
+        la.conv_cin, la.conv_tin, la.conv_tout, la.conv_stride = g.n_mels, 3000, 3000, 1
+    elif name == "conv2":
+        la.epilogue, la.k, la.pos = L.EPI_GELU_POS, 3 * d, pos
+        la.conv_cin, la.conv_tin, la.conv_tout, la.conv_stride = d, 3000, 1500, 2
+    elif name == "xkv":
+        la.epilogue, la.n, la.heads, la.blocks_per_clip, la.nh, la.kind = (L.EPI_HEADS, g.dec_layers * 2 * d, heads,
+                                                                         g.dec_layers * 2 * nh, nh, 2)
+    elif name not in ("attn", "ln"):
+        raise SystemExit(f"unknown probe {name}")
+    lw, lb = ctx.upload_new(np.ones(d, np.float16)), ctx.upload_new(np.zeros(d, np.float16))
+    for _ in range(reps):
+        if name == "attn":
+            L.check(L.lib().mz_enc_attention(ctx.h, heads, out, EG, nh))
+        elif name == "ln":
+            L.check(L.lib().mz_add_layernorm(ctx.h, out, x, lw, lb, heads, M, d, 1e-5))
+        else:
+            L.check(L.lib().mz_linear(ctx.h, C.byref(la)))
+    ctx.sync()
+    bound, amount = kernel_work(g, EG)[name]
+    print(json.dumps({"probe": name, "launches": reps, "algorithmic": amount, "bound": bound}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -123,7 +186,12 @@ def main():
     ap.add_argument("--no-graph", action="store_true",
                     help="launch every decoder step's kernels instead of replaying the captured graph (as the "
                          "reference's --no-graph; for kernel tracers that do not follow graph launches)")
+    ap.add_argument("--probe", default=None,
+                    help="run one kernel class at the bench shape (or 'copy') for counter runs, then exit")
     a = ap.parse_args()
+    if a.probe:
+        probe(a.probe)
+        return
     if a.gpus != 1:
         print("bench.py measures one GPU: this path shards over clips with no exchange step, and multi-GPU runs "
               "are not part of this build (use --gpus 1)", file=sys.stderr)
@@ -186,9 +254,16 @@ def main():
     dk = kernels[dom]
     bound, amount = work[dom]
     avg = dk["avg_us"] * 1e-6
+    traffic, traffic_src = None, None
+    tf = os.path.join(ROOT, "profiles", "traffic.json")  # HBM bytes per launch from rocprofv3 FETCH/WRITE_SIZE runs
+    if os.path.exists(tf):
+        with open(tf) as f:
+            t = json.load(f).get(dom)
+        if t:
+            traffic, traffic_src = t["bytes_per_launch"], t["source"]
     roof = {"kernel": dom, "bound": bound, "achieved": round(amount / avg / (1e12 if bound == "mfma" else 1e9), 2),
             "peak": 2500.0 if bound == "mfma" else 8000.0, "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
-            "frac": dk["frac"], "traffic": None,
+            "frac": dk["frac"], "traffic": traffic, "traffic_source": traffic_src,
             "per_launch": f"{amount / 1e9:.2f} G{'FLOP' if bound == 'mfma' else 'B'} ({EG} clips x 1500 frames)"}
 
     # decoder step alone at the 32-row batch, positions 200..219 (self-attention cache of 201..220 entries)

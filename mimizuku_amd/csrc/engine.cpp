@@ -78,6 +78,7 @@ struct mz_engine {
     // encoder scratch (eg clips)
     float* mel = nullptr;
     f16 *melT = nullptr, *h1 = nullptr, *hb = nullptr, *qkvh = nullptr, *att = nullptr, *ff = nullptr;
+    f16* dd = nullptr;  // out-projection / fc2 output, added to the residual stream by the next add + LayerNorm
     float *ex = nullptr, *trace = nullptr;
     // decoder state (bmax rows)
     f16* xkvbuf = nullptr;
@@ -165,7 +166,7 @@ extern "C" size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int 
     const size_t D = d->d, F = d->ff, nl = d->dec_layers, nh = d->nh, mt = d->max_t, V = d->vocab;
     const size_t B = bmax, G = eg;
     size_t enc = G * d->n_mels * NFR * 4 + G * NFR * d->n_mels * 2 + G * NFR * D * 2 + G * TENC * D * 4 +
-                 G * TENC * D * 2 * 2 + G * 3 * nh * TPAD * HD * 2 + G * TENC * F * 2;
+                 G * TENC * D * 2 * 3 + G * 3 * nh * TPAD * HD * 2 + G * TENC * F * 2;
     size_t dec = B * nl * 2 * nh * TPAD * HD * 2 + B * mt * 4 + B * 4 + 16 + B * D * 4 * 2 + B * D * 2 * 2 + B * F * 2 +
                  2 * nl * B * nh * mt * HD * 2 + B * V * 4 + B * mt * n_align * TENC * 4 + (V + MZ_LM_COLS - 1) / MZ_LM_COLS * B * 8 +
                  nl * nh * 4 + 2 * V;
@@ -303,7 +304,8 @@ extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, in
     if ((r = e->alloc(&e->mel, G * d->n_mels * NFR)) || (r = e->alloc(&e->melT, G * NFR * d->n_mels)) ||
         (r = e->alloc(&e->h1, G * NFR * D)) || (r = e->alloc(&e->ex, G * TENC * D)) ||
         (r = e->alloc(&e->hb, G * TENC * D)) || (r = e->alloc(&e->qkvh, G * 3 * nh * (size_t)TPAD * HD)) ||
-        (r = e->alloc(&e->att, G * TENC * D)) || (r = e->alloc(&e->ff, G * TENC * F)))
+        (r = e->alloc(&e->att, G * TENC * D)) || (r = e->alloc(&e->ff, G * TENC * F)) ||
+        (r = e->alloc(&e->dd, G * TENC * D)))
         return fail(r);
     if ((r = e->alloc(&e->xkvbuf, B * nl * 2 * nh * (size_t)TPAD * HD)) || (r = e->alloc(&e->tok, B * mt)) ||
         (r = e->alloc(&e->done, B)) || (r = e->alloc(&e->ctr, 4)) || (r = e->alloc(&e->x, B * D)) ||
@@ -489,10 +491,12 @@ static int encode_impl(mz_engine* e, const float* mels, bool on_device, int n, i
         g.M = rows;
         g.N = D;
         g.K = D;
-        g.out = e->ex;
+        g.out = e->dd;
         g.ldo = D;
-        PROF(MZ_K_OPROJ, mz_gemm_launch(s, ALOAD_PLAIN, EPI_RESID_F32, g), "out-proj");
-        PROF(MZ_K_LN, mz_layernorm_launch(s, e->ex, D, L.ln2.w, L.ln2.b, e->hb, D, rows, D, EPS), "ln2");
+        // the projection's output is rounded to fp16 once (as the reference's linear outputs) and added to the fp32
+        // residual stream by the streaming add + LayerNorm, which also normalises for fc1
+        PROF(MZ_K_OPROJ, mz_gemm_launch(s, ALOAD_PLAIN, EPI_F16, g), "out-proj");
+        PROF(MZ_K_LN, mz_add_layernorm_launch(s, e->ex, e->dd, L.ln2.w, L.ln2.b, e->hb, rows, D, EPS), "add+ln2");
         g.A = e->hb;
         g.W = L.fc1.w;
         g.bias = L.fc1.b;
@@ -506,11 +510,11 @@ static int encode_impl(mz_engine* e, const float* mels, bool on_device, int n, i
         g.bias = L.fc2.b;
         g.N = D;
         g.K = F;
-        g.out = e->ex;
+        g.out = e->dd;
         g.ldo = D;
-        PROF(MZ_K_FC2, mz_gemm_launch(s, ALOAD_PLAIN, EPI_RESID_F32, g), "fc2");
+        PROF(MZ_K_FC2, mz_gemm_launch(s, ALOAD_PLAIN, EPI_F16, g), "fc2");
         const Ln& nx = i + 1 < e->dm.enc_layers ? e->encv[i + 1].ln1 : e->eln;  // the last one is the final LN
-        PROF(MZ_K_LN, mz_layernorm_launch(s, e->ex, D, nx.w, nx.b, e->hb, D, rows, D, EPS), "ln");
+        PROF(MZ_K_LN, mz_add_layernorm_launch(s, e->ex, e->dd, nx.w, nx.b, e->hb, rows, D, EPS), "add+ln");
     }
     // cross k/v of every decoder layer for the clips' slots (src/model.rs:614-623)
     g = MzGemm{};
@@ -799,7 +803,7 @@ extern "C" int mz_engine_free(mz_engine* e) {
     }
     for (hipEvent_t x : e->evpool) hipEventDestroy(x);
     if (e->align_host) hipHostFree(e->align_host);
-    for (void* p : {(void*)e->arena, (void*)e->mel, (void*)e->melT, (void*)e->h1, (void*)e->ex, (void*)e->hb,
+    for (void* p : {(void*)e->arena, (void*)e->mel, (void*)e->melT, (void*)e->h1, (void*)e->ex, (void*)e->hb, (void*)e->dd,
                     (void*)e->qkvh, (void*)e->att, (void*)e->ff, (void*)e->trace, (void*)e->xkvbuf, (void*)e->tok,
                     (void*)e->done, (void*)e->ctr, (void*)e->x, (void*)e->q, (void*)e->h, (void*)e->datt,
                     (void*)e->dff, (void*)e->kc, (void*)e->vc, (void*)e->logits, (void*)e->align, (void*)e->amax,

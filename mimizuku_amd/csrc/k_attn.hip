@@ -20,11 +20,16 @@ constexpr int NT = MZ_TPAD / 64;  // key tiles (the last one holds keys 1472..15
 
 __device__ __forceinline__ int swap23(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
 
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) enc_attn_kernel(const f16* __restrict__ qkvh, f16* __restrict__ out, int nh) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) enc_attn_kernel(const f16* __restrict__ qkvh, f16* __restrict__ out, int nh, int G) {
     __shared__ __attribute__((aligned(16))) f16 sK[2][64 * KP];
     __shared__ __attribute__((aligned(16))) f16 sV[2][64 * KP];
 
-    const int head = blockIdx.y, g = blockIdx.z;
+    // workgroup i runs on XCD i % 8: XCD x takes (clip, head) pairs x, x + 8, ... and all six query blocks of a pair,
+    // so a pair's K and V tiles are fetched into one L2 only
+    const int xcd = blockIdx.x & 7, li = blockIdx.x >> 3, npq = (MZ_TENC + QB - 1) / QB;
+    const int pair = (li / npq) * 8 + xcd, qb = li % npq;
+    if (pair >= nh * G) return;
+    const int head = pair % nh, g = pair / nh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, lh = lane >> 5;
     const long blk = (long)MZ_TPAD * MZ_HD;
     const f16* Q = qkvh + ((long)g * 3 * nh + head) * blk;
@@ -33,7 +38,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int d = nh * MZ_HD;
 
     // query fragments (B operand of S^T): query row, dims 16c + 8 lh .. + 8
-    const int q0 = blockIdx.x * QB + wave * 64;
+    const int q0 = qb * QB + wave * 64;
     f16x8 qf[2][4];
 #pragma unroll
     for (int s = 0; s < 2; s++)
@@ -146,7 +151,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 
 hipError_t mz_enc_attention_launch(hipStream_t s, const f16* qkvh, f16* out, int G, int nh) {
     if (G <= 0 || nh <= 0) return hipErrorInvalidValue;
-    dim3 grid((MZ_TENC + QB - 1) / QB, nh, G);
-    hipLaunchKernelGGL(enc_attn_kernel, grid, dim3(256), 0, s, qkvh, out, nh);
+    // 1-D grid: 8 XCDs x ceil(pairs / 8) pairs x 6 query blocks
+    const int npq = (MZ_TENC + QB - 1) / QB, pairs = G * nh;
+    hipLaunchKernelGGL(enc_attn_kernel, dim3(8 * ((pairs + 7) / 8) * npq), dim3(256), 0, s, qkvh, out, nh, G);
     return hipGetLastError();
 }

@@ -28,11 +28,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigne
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// Map the launch index to a tile so that the blocks one XCD receives (block i runs on XCD i % 8) form a contiguous
-// run of tiles, ordered with N fastest: concurrently resident blocks of an XCD share activation rows in its L2.
-__device__ __forceinline__ int xcd_tile(int bid, int nblocks) {
-    int per = nblocks >> 3;
-    return (bid & 7) * per + (bid >> 3);
+// Workgroup i runs on XCD i % 8, and each XCD has its own L2. XCD x owns a band of rows = ceil(nbm / 8) block rows
+// and visits its tiles with the block row fastest: the band's activation panels stay in its L2 while each weight
+// panel is read once per XCD and shared by the band's tiles that run at the same time. The grid is 8 * rows * nbn.
+__device__ __forceinline__ bool xcd_tile(int bid, int nbm, int nbn, int* bm, int* bn) {
+    const int rows = (nbm + 7) >> 3, li = bid >> 3;
+    *bm = (bid & 7) * rows + li % rows;
+    *bn = li / rows;
+    return *bm < nbm && *bn < nbn;
 }
 
 template <int BM, int BN, int ALOAD, int EPI>
@@ -47,9 +50,8 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
     __shared__ __attribute__((aligned(16))) f16 sW1[BN * 64];
 
     const int nbn = (p.N + BN - 1) / BN, nbm = (p.M + BM - 1) / BM;
-    const int tile = xcd_tile(blockIdx.x, gridDim.x);
-    if (tile >= nbm * nbn) return;
-    const int bm = tile / nbn, bn = tile % nbn;
+    int bm, bn;
+    if (!xcd_tile(blockIdx.x, nbm, nbn, &bm, &bn)) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 2, wn = wave & 3, lr = lane & 31, lh = lane >> 5;
     const int nk = p.K >> 6;
@@ -217,8 +219,8 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
 
 template <int BM, int BN, int ALOAD, int EPI>
 hipError_t launch(hipStream_t s, const MzGemm& g) {
-    int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-    int grid = (tiles + 7) & ~7;
+    const int nbm = (g.M + BM - 1) / BM, nbn = (g.N + BN - 1) / BN;
+    const int grid = 8 * ((nbm + 7) / 8) * nbn;
     hipLaunchKernelGGL((gemm_kernel<BM, BN, ALOAD, EPI>), dim3(grid), dim3(NW * 64), 0, s, g);
     return hipGetLastError();
 }

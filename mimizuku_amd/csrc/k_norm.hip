@@ -1,73 +1,82 @@
 // Row LayerNorm kernels over the fp32 residual stream, and the log-mel layout change for the conv stem.
 // LayerNorm follows kernels/whisper.cu:48-82 (two-pass fp32 statistics, eps 1e-5, biased variance) with one wave64
-// per row: the row is held in registers (dim / 128 float2 per lane), so it is read from HBM once.
+// per row: the row is held in registers (dim / 256 float4 per lane), so it is read from HBM once.
 #include "mz_common.h"
 #include "mz_kernels.h"
 
 namespace {
 
-constexpr int MAXV = 16;  // float2 per lane: dim <= 2048
+constexpr int MAXC = 8;  // float4 chunks per lane: dim <= 2048
 
-// LayerNorm of one row held as v[i] = x[(lane + 64 i) * 2 .. + 2], written to y as fp16.
-__device__ __forceinline__ void ln_store(const float2 (&v)[MAXV], int nv, int lane, const f16* w, const f16* b, f16* y,
-                                         int dim, float eps) {
+// LayerNorm of one row held as v[i] = x[4 (lane + 64 i) .. + 4] (chunks past dim / 4 hold zeros and are not
+// stored), written to y as fp16. Two-pass statistics (mean, then the centred second moment) as the reference.
+__device__ __forceinline__ void ln_store(const float4 (&v)[MAXC], int nc, int lane, const f16* __restrict__ w,
+                                         const f16* __restrict__ b, f16* __restrict__ y, int dim, float eps) {
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < MAXV; i++)
-        if (i < nv) s += v[i].x + v[i].y;
+    for (int i = 0; i < MAXC; i++)
+        if (lane + 64 * i < nc) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
     const float mean = wave_sum(s) / dim;
     float q = 0.f;
 #pragma unroll
-    for (int i = 0; i < MAXV; i++)
-        if (i < nv) {
-            float a = v[i].x - mean, c = v[i].y - mean;
-            q += a * a + c * c;
+    for (int i = 0; i < MAXC; i++)
+        if (lane + 64 * i < nc) {
+            const float a = v[i].x - mean, c = v[i].y - mean, e = v[i].z - mean, f = v[i].w - mean;
+            q += (a * a + c * c) + (e * e + f * f);
         }
     const float rstd = rsqrtf(wave_sum(q) / dim + eps);
 #pragma unroll
-    for (int i = 0; i < MAXV; i++)
-        if (i < nv) {
-            int idx = (lane + 64 * i) * 2;
-            f16x2 wv = *(const f16x2*)(w + idx), bv = *(const f16x2*)(b + idx);
-            f16x2 o = {(f16)((v[i].x - mean) * rstd * (float)wv[0] + (float)bv[0]),
-                       (f16)((v[i].y - mean) * rstd * (float)wv[1] + (float)bv[1])};
-            *(f16x2*)(y + idx) = o;
+    for (int i = 0; i < MAXC; i++)
+        if (lane + 64 * i < nc) {
+            const int idx = (lane + 64 * i) * 4;
+            const f16x4 wv = *(const f16x4*)(w + idx), bv = *(const f16x4*)(b + idx);
+            st4(y + idx, (v[i].x - mean) * rstd * (float)wv[0] + (float)bv[0],
+                (v[i].y - mean) * rstd * (float)wv[1] + (float)bv[1], (v[i].z - mean) * rstd * (float)wv[2] + (float)bv[2],
+                (v[i].w - mean) * rstd * (float)wv[3] + (float)bv[3]);
         }
 }
 
-__global__ void __launch_bounds__(256) ln_kernel(const float* x, long ldx, const f16* w, const f16* b, f16* y, long ldy,
-                                                 int rows, int dim, float eps) {
+// one wave per row, 4 rows per workgroup; every load of the row is issued before the reductions
+__global__ void __launch_bounds__(256) ln_kernel(const float* __restrict__ x, long ldx, const f16* __restrict__ w,
+                                                 const f16* __restrict__ b, f16* __restrict__ y, long ldy, int rows,
+                                                 int dim, float eps) {
     const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
-    const int nv = dim / 128;
+    const int nc = dim / 4;
     const float* xr = x + (long)row * ldx;
-    float2 v[MAXV];
+    float4 v[MAXC];
 #pragma unroll
-    for (int i = 0; i < MAXV; i++)
-        if (i < nv) v[i] = *(const float2*)(xr + (lane + 64 * i) * 2);
-    ln_store(v, nv, lane, w, b, y + (long)row * ldy, dim, eps);
+    for (int i = 0; i < MAXC; i++) v[i] = lane + 64 * i < nc ? *(const float4*)(xr + (lane + 64 * i) * 4) : float4{};
+    ln_store(v, nc, lane, w, b, y + (long)row * ldy, dim, eps);
 }
 
-__global__ void __launch_bounds__(256) add_ln_kernel(float* x, const f16* d, const f16* w, const f16* b, f16* y,
-                                                     int rows, int dim, float eps) {
+// x[r] += d[r] (fp16) in place, then y[r] = LN(x[r])
+__global__ void __launch_bounds__(256) add_ln_kernel(float* __restrict__ x, const f16* __restrict__ d,
+                                                     const f16* __restrict__ w, const f16* __restrict__ b,
+                                                     f16* __restrict__ y, int rows, int dim, float eps) {
     const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
-    const int nv = dim / 128;
+    const int nc = dim / 4;
     float* xr = x + (long)row * dim;
     const f16* dr = d + (long)row * dim;
-    float2 v[MAXV];
+    float4 v[MAXC];
+    f16x4 dv[MAXC];
 #pragma unroll
-    for (int i = 0; i < MAXV; i++)
-        if (i < nv) {
-            int idx = (lane + 64 * i) * 2;
-            float2 a = *(const float2*)(xr + idx);
-            f16x2 c = *(const f16x2*)(dr + idx);
-            a.x += (float)c[0];
-            a.y += (float)c[1];
-            *(float2*)(xr + idx) = a;
-            v[i] = a;
+    for (int i = 0; i < MAXC; i++) {
+        const bool on = lane + 64 * i < nc;
+        v[i] = on ? *(const float4*)(xr + (lane + 64 * i) * 4) : float4{};
+        dv[i] = on ? *(const f16x4*)(dr + (lane + 64 * i) * 4) : f16x4{};
+    }
+#pragma unroll
+    for (int i = 0; i < MAXC; i++)
+        if (lane + 64 * i < nc) {
+            v[i].x += (float)dv[i][0];
+            v[i].y += (float)dv[i][1];
+            v[i].z += (float)dv[i][2];
+            v[i].w += (float)dv[i][3];
+            *(float4*)(xr + (lane + 64 * i) * 4) = v[i];
         }
-    ln_store(v, nv, lane, w, b, y + (long)row * dim, dim, eps);
+    ln_store(v, nc, lane, w, b, y + (long)row * dim, dim, eps);
 }
 
 // mel f32 [G][nm][3000] -> f16 [G][3000][nm], 64 x 64 tiles through LDS
@@ -91,14 +100,14 @@ __global__ void __launch_bounds__(256) mel_t_kernel(const float* mel, f16* melT,
 
 hipError_t mz_layernorm_launch(hipStream_t s, const float* x, long ldx, const f16* w, const f16* b, f16* y, long ldy,
                                int rows, int dim, float eps) {
-    if (dim % 128 != 0 || dim > 128 * MAXV || rows <= 0) return hipErrorInvalidValue;
+    if (dim % 4 != 0 || dim > 256 * MAXC || rows <= 0 || ldx % 4 != 0 || ldy % 4 != 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(ln_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, ldx, w, b, y, ldy, rows, dim, eps);
     return hipGetLastError();
 }
 
 hipError_t mz_add_layernorm_launch(hipStream_t s, float* x, const f16* d, const f16* w, const f16* b, f16* y, int rows,
                                    int dim, float eps) {
-    if (dim % 128 != 0 || dim > 128 * MAXV || rows <= 0) return hipErrorInvalidValue;
+    if (dim % 4 != 0 || dim > 256 * MAXC || rows <= 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(add_ln_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, d, w, b, y, rows, dim, eps);
     return hipGetLastError();
 }

@@ -14,7 +14,9 @@ How each part is pinned (tests/test_oracle.py):
   * attention: against a float64 closed form and against permutation invariance of keys;
   * layer_norm / gelu: against closed forms (math.erf) and invariants (zero mean, unit variance);
   * conv1d: against a brute-force loop on a tiny input;
-  * dtw / median filter / jump_times: against the reference's KATs (src/align.rs:112-139) and brute force.
+  * dtw / median filter / jump_times: against the reference's KATs (src/align.rs:112-139) and brute force;
+  * choose / top2_margin: hand-made logit vectors with known answers (ties, suppression, begin-suppression);
+  * rh (fp16 rounding): known answers of IEEE round-to-nearest-even (ties, overflow, subnormal ties).
 """
 from __future__ import annotations
 

@@ -175,3 +175,17 @@ def test_choose_rules():
     assert R.choose(lg, {4}, [1], False, 0, False) == 1
     assert R.choose(lg, {0, 1, 2, 3, 4}, [], False, 7, False) == 7  # all suppressed -> eos
     assert R.choose(lg, set(), [], False, 7, True) == 7  # finished row -> eos
+
+
+def test_top2_margin_closed_form():
+    lg = np.array([0.5, 3.0, -1.0, 2.25, 7.0], np.float32)
+    assert R.top2_margin(lg, {4}, [], False) == 0.75  # 3.0 - 2.25 once id 4 is suppressed
+    assert R.top2_margin(lg, set(), [4], True) == 0.75  # begin-suppressed at the first position
+    assert R.top2_margin(lg, set(), [4], False) == 4.0  # but not later: 7.0 - 3.0
+
+
+def test_fp16_rounding_known_answers():
+    assert R.rh(1.0 + 2.0 ** -11) == 1.0  # a tie rounds to even
+    assert R.rh(1.0 + 3.0 * 2.0 ** -11) == 1.0 + 2.0 ** -9
+    assert R.rh(65519.0) == 65504.0 and np.isinf(R.rh(65520.0))
+    assert R.rh(2.0 ** -25) == 0.0 and R.rh(3.0 * 2.0 ** -25) == 2.0 ** -23  # subnormal ties
