@@ -219,6 +219,14 @@ int mz_transcribe_device(mz_engine* e, uint64_t mels, const int32_t* frames, int
                          int prompt_len, int detect, int use_graph, int max_new, int half_align, int32_t* seq,
                          int32_t* seq_len, float* ts, int32_t* langs, mz_times* times);
 
+/* Token start times of n clips on the device, the same bits as mz_jump_times on each clip (jump_times,
+ * src/align.rs:8-63; the reference runs it on the host after downloading the weights, transcribe.rs:150-158).
+ * Clip c's alignment-head weights are rows[c] rows of heads x cols_full floats at device address
+ * w + c * clip_stride * 4, cropped to cols[c] frames; its times go to host out[c * out_stride + k], k < rows[c].
+ * Odd width <= 15. Allocates and frees its own device scratch; synchronous on the context's stream. */
+int mz_jump_times_device(mz_ctx* c, uint64_t w, int64_t clip_stride, int n, const int32_t* rows, const int32_t* cols,
+                         int heads, int cols_full, int width, int half, float* out, int64_t out_stride);
+
 /* ------------------------------------------------------------------ host helpers */
 
 /* Token start times from alignment-head weights w [rows][heads][cols_full] (f32), cropped to cols frames

@@ -110,9 +110,11 @@ struct mz_engine {
         if (hipEventCreate(&x) != hipSuccess) return nullptr;
         return x;
     }
-    // pinned host staging of the alignment rows read back after decoding (hipHostMalloc'd on first use)
-    float* align_host = nullptr;
-    size_t align_host_bytes = 0;
+    // token timestamps (k_align.hip): per clip (rows, columns), column statistics, DTW cost and trace in
+    // anti-diagonal-major order for up to max_t - 1 rows, and the start time of every row
+    int2* ts_rc = nullptr;
+    float *ts_mean = nullptr, *ts_sd = nullptr, *ts_cost = nullptr, *ts_out = nullptr;
+    signed char* ts_trace = nullptr;
     // position of the next step as the host has enqueued it (the device copy is ctr[0]); steps beyond the cache
     // (max_t - 1 of them after a reset) are refused
     int host_pos = 0;
@@ -171,7 +173,8 @@ extern "C" size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int 
                  2 * nl * B * nh * mt * HD * 2 + B * V * 4 + B * mt * n_align * TENC * 4 + (V + MZ_LM_COLS - 1) / MZ_LM_COLS * B * 8 +
                  nl * nh * 4 + 2 * V;
     size_t part = (size_t)MZ_MAX_PARTS * B * D * 4;
-    return enc + dec + part;
+    size_t ts = B * 8 + 2 * B * n_align * TENC * 4 + B * (size_t)mz_ts_diag_stride((int)mt - 1, TENC) * 5 + B * mt * 4;
+    return enc + dec + part + ts;
 }
 
 extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, int bmax, int eg, mz_engine** out) {
@@ -315,6 +318,11 @@ extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, in
         (r = e->alloc(&e->align, B * mt * e->na * (size_t)TENC)) ||
         (r = e->alloc(&e->amax, (size_t)((V + MZ_LM_COLS - 1) / MZ_LM_COLS) * B)) ||
         (r = e->alloc(&e->aslot, (size_t)nl * nh)) || (r = e->alloc(&e->sup, V)) || (r = e->alloc(&e->sup_lang, V)))
+        return fail(r);
+    const size_t tsd = (size_t)mz_ts_diag_stride(mt - 1, TENC);
+    if ((r = e->alloc(&e->ts_rc, B)) || (r = e->alloc(&e->ts_mean, B * e->na * (size_t)TENC)) ||
+        (r = e->alloc(&e->ts_sd, B * e->na * (size_t)TENC)) || (r = e->alloc(&e->ts_cost, B * tsd)) ||
+        (r = e->alloc(&e->ts_trace, B * tsd)) || (r = e->alloc(&e->ts_out, B * mt)))
         return fail(r);
     // split-K partials: the largest ks * rows * n over the decoder products
     size_t pe = 0;
@@ -802,7 +810,6 @@ extern "C" int mz_engine_free(mz_engine* e) {
         hipEventDestroy(r.b);
     }
     for (hipEvent_t x : e->evpool) hipEventDestroy(x);
-    if (e->align_host) hipHostFree(e->align_host);
     for (void* p : {(void*)e->arena, (void*)e->mel, (void*)e->melT, (void*)e->h1, (void*)e->ex, (void*)e->hb, (void*)e->dd,
                     (void*)e->qkvh, (void*)e->att, (void*)e->ff, (void*)e->trace, (void*)e->xkvbuf, (void*)e->tok,
                     (void*)e->done, (void*)e->ctr, (void*)e->x, (void*)e->q, (void*)e->h, (void*)e->datt,
@@ -872,9 +879,11 @@ static int transcribe_impl(mz_engine* e, const float* mels, bool on_device, cons
     std::vector<int32_t> toks((size_t)n * mt);
     if (int r = mz_download(e->c, toks.data(), (uint64_t)(uintptr_t)e->tok, toks.size() * 4)) return r;
     const size_t row = (size_t)e->na * TENC;
-    // sequence lengths, then the alignment rows of every clip into pinned memory in one batch of copies
+    // sequence lengths; the token rows of clip c are the positions np .. n_seq - 2 (the last token is eos or the
+    // step limit) and their alignment rows start at align[c][np]
     std::vector<int> nseq(n), nrows(n);
-    std::vector<size_t> off(n + 1, 0);
+    std::vector<int2> rc(n);
+    int rmax = 0;
     for (int c = 0; c < n; c++) {
         const int32_t* t = &toks[(size_t)c * mt];
         int n_seq = std::min(steps + 1, mt);
@@ -886,41 +895,37 @@ static int transcribe_impl(mz_engine* e, const float* mels, bool on_device, cons
         n_seq = std::min(n_seq, steps + 1);
         nseq[c] = n_seq;
         nrows[c] = std::max(n_seq - 1 - np, 0);
-        off[c + 1] = off[c] + (size_t)nrows[c] * row;
+        rc[c] = int2{nrows[c], frames[c] / 2};
+        rmax = std::max(rmax, nrows[c]);
     }
-    if (off[n] * 4 > e->align_host_bytes) {
-        if (e->align_host) hipHostFree(e->align_host);
-        e->align_host = nullptr;
-        e->align_host_bytes = 0;
-        const size_t want = (size_t)e->bmax * mt * row * 4;
-        TRY(hipHostMalloc((void**)&e->align_host, want, hipHostMallocDefault), "hipHostMalloc");
-        e->align_host_bytes = want;
+    // token timestamps on the device (median filter + DTW per clip, k_align.hip); only the times come back
+    std::vector<float> jt((size_t)n * mt);
+    if (rmax > 0) {
+        TRY(hipMemcpyAsync(e->ts_rc, rc.data(), (size_t)n * sizeof(int2), hipMemcpyHostToDevice, e->c->stream),
+            "upload");
+        MzTs p{};
+        p.w = e->align + (size_t)np * row;
+        p.clip_stride = (long)mt * row;
+        p.heads = e->na;
+        p.cols_full = TENC;
+        p.width = 7;
+        p.half = half_align;
+        p.rmax = rmax;
+        p.rc = e->ts_rc;
+        p.mean = e->ts_mean;
+        p.sd = e->ts_sd;
+        p.cost = e->ts_cost;
+        p.trace = e->ts_trace;
+        p.diag_stride = mz_ts_diag_stride(rmax, TENC);
+        p.ldd = rmax + 1;
+        p.out = e->ts_out;
+        p.out_stride = mt;
+        TRY(mz_ts_launch(e->c->stream, p, n), "timestamp kernels");
+        TRY(hipMemcpyAsync(jt.data(), e->ts_out, jt.size() * 4, hipMemcpyDeviceToHost, e->c->stream),
+            "timestamp download");
+        if (int r = mz_sync(e->c)) return r;
     }
-    for (int c = 0; c < n; c++)
-        if (nrows[c] > 0)
-            TRY(hipMemcpyAsync(e->align_host + off[c], e->align + ((size_t)c * mt + np) * row,
-                               (size_t)nrows[c] * row * 4, hipMemcpyDeviceToHost, e->c->stream),
-                "align download");
-    if (int r = mz_sync(e->c)) return r;
-    // token timestamps per clip (median filter + DTW on the host), clips in parallel
-    std::vector<std::vector<float>> jts(n);
-    std::vector<int> rcs(n, MZ_OK);
-    std::atomic<int> next{0};
-    auto work = [&]() {
-        for (int c; (c = next.fetch_add(1)) < n;) {
-            if (nrows[c] <= 0) continue;
-            jts[c].resize(nrows[c]);
-            rcs[c] = mz_jump_times(e->align_host + off[c], nrows[c], e->na, TENC, frames[c] / 2, 7, half_align,
-                                       jts[c].data());
-        }
-    };
-    const int nth = std::max(1, std::min({n, (int)std::thread::hardware_concurrency(), 16}));
-    std::vector<std::thread> pool;
-    for (int t = 1; t < nth; t++) pool.emplace_back(work);
-    work();
-    for (auto& th : pool) th.join();
     for (int c = 0; c < n; c++) {
-        if (rcs[c]) return rcs[c];
         const int32_t* t = &toks[(size_t)c * mt];
         const int n_seq = nseq[c];
         for (int k = 0; k < mt; k++) seq[(size_t)c * mt + k] = k < n_seq ? t[k] : 0;
@@ -929,8 +934,9 @@ static int transcribe_impl(mz_engine* e, const float* mels, bool on_device, cons
         std::fill(tc, tc + mt, 0.f);
         const int rows = nrows[c];
         if (rows > 0) {
-            for (int k = 0; k < rows; k++) tc[np + k] = jts[c][k];
-            tc[n_seq - 1] = jts[c][rows - 1];
+            const float* j = &jt[(size_t)c * mt];
+            for (int k = 0; k < rows; k++) tc[np + k] = j[k];
+            tc[n_seq - 1] = j[rows - 1];
         }
         langs[c] = lg[c];
     }

@@ -119,3 +119,26 @@ hipError_t mz_dec_embed_ln_launch(hipStream_t s, const int* tok, int* ctr, const
 // greedy choice of token p + 1 (kernels/whisper.cu:451-493 semantics) from the LM head partials; ctr[0] = p + 1
 hipError_t mz_dec_argmax_launch(hipStream_t s, const int2* amax, int nblk, int* tok, int* done, int* ctr, int B,
                                 int maxT, int prompt_len, int eos);
+
+// ---------------------------------------------------------------- token timestamps
+// Alignment rows of clip c: w + c * clip_stride floats, rc[c].x rows of heads x cols_full floats, of which the first
+// rc[c].y columns are used. Scratch per clip: mean and sd [heads][cols_full]; cost (f32) and trace (i8) in
+// anti-diagonal-major order [rmax + cols_full + 1][ldd], ldd >= rmax + 1, diag_stride elements apart.
+#define MZ_TS_MAX_WIDTH 15
+struct MzTs {
+    const float* w;
+    long clip_stride;
+    int heads, cols_full, width, half, rmax;
+    const int2* rc;
+    float* mean;
+    float* sd;
+    float* cost;
+    signed char* trace;
+    long diag_stride;
+    int ldd;
+    float* out;  // out[c * out_stride + k], k < rc[c].x: start time in seconds of row k's token
+    long out_stride;
+};
+// scratch elements per clip for cost / trace
+inline long mz_ts_diag_stride(int rmax, int cols_full) { return (long)(rmax + cols_full + 1) * (rmax + 1); }
+hipError_t mz_ts_launch(hipStream_t s, const MzTs& p, int n);

@@ -9,6 +9,8 @@
 #include <mutex>
 #include <set>
 #include <string>
+#include <vector>
+#include <algorithm>
 
 #include "../../include/mimizuku.h"
 #include "mz_internal.h"
@@ -285,4 +287,66 @@ extern "C" int mz_enc_attention(mz_ctx* c, uint64_t qkvh, uint64_t out, int clip
 extern "C" int mz_mel_transpose(mz_ctx* c, uint64_t mel, uint64_t melT, int clips, int n_mels) {
     if (!c) return mz_fail(MZ_ERR_ARG, "mz_mel_transpose: null ctx");
     return mz_hip(mz_mel_transpose_launch(c->stream, CDP(float, mel), (f16*)DP(melT), clips, n_mels), "mz_mel_transpose");
+}
+
+// ------------------------------------------------------------------ token timestamps on the device
+
+extern "C" int mz_jump_times_device(mz_ctx* c, uint64_t w, int64_t clip_stride, int n, const int32_t* rows,
+                                    const int32_t* cols, int heads, int cols_full, int width, int half, float* out,
+                                    int64_t out_stride) {
+    if (!c || !w || !rows || !cols || !out || n < 0 || heads <= 0 || cols_full <= 0 || clip_stride < 0)
+        return mz_fail(MZ_ERR_ARG, "mz_jump_times_device: bad argument");
+    if (width < 1 || width % 2 == 0 || width > MZ_TS_MAX_WIDTH)
+        return mz_fail(MZ_ERR_ARG, "mz_jump_times_device: width %d (odd, at most %d)", width, MZ_TS_MAX_WIDTH);
+    if (n == 0) return MZ_OK;
+    int rmax = 0;
+    std::vector<int2> rc(n);
+    for (int i = 0; i < n; i++) {
+        if (rows[i] < 0 || cols[i] < 0 || cols[i] > cols_full || rows[i] > 4095 || rows[i] > out_stride)
+            return mz_fail(MZ_ERR_ARG, "mz_jump_times_device: clip %d has %d rows, %d columns", i, rows[i], cols[i]);
+        rc[i] = int2{rows[i], cols[i]};
+        rmax = std::max(rmax, rows[i]);
+    }
+    if (int r = mz_hip(hipSetDevice(c->device), "hipSetDevice")) return r;
+    const long ds = mz_ts_diag_stride(rmax, cols_full);
+    const size_t stat = (size_t)n * heads * cols_full;
+    const size_t bytes[5] = {(size_t)n * sizeof(int2), stat * 4, stat * 4, (size_t)n * ds * 5,
+                             (size_t)n * out_stride * 4};
+    void* buf[5] = {};
+    auto release = [&]() {
+        for (void* b : buf)
+            if (b) hipFree(b);
+    };
+    for (int i = 0; i < 5; i++)
+        if (int r = mz_hip(hipMalloc(&buf[i], std::max<size_t>(bytes[i], 4)), "hipMalloc")) {
+            release();
+            return r;
+        }
+    MzTs p{};
+    p.w = (const float*)(uintptr_t)w;
+    p.clip_stride = clip_stride;
+    p.heads = heads;
+    p.cols_full = cols_full;
+    p.width = width;
+    p.half = half;
+    p.rmax = rmax;
+    p.rc = (const int2*)buf[0];
+    p.mean = (float*)buf[1];
+    p.sd = (float*)buf[2];
+    p.cost = (float*)buf[3];
+    p.trace = (signed char*)((float*)buf[3] + (size_t)n * ds);
+    p.diag_stride = ds;
+    p.ldd = rmax + 1;
+    p.out = (float*)buf[4];
+    p.out_stride = out_stride;
+    int r = mz_hip(hipMemcpyAsync(buf[0], rc.data(), bytes[0], hipMemcpyHostToDevice, c->stream), "upload");
+    if (!r) r = mz_hip(mz_ts_launch(c->stream, p, n), "timestamp kernels");
+    for (int i = 0; i < n && !r; i++)
+        if (rows[i] > 0)
+            r = mz_hip(hipMemcpyAsync(out + i * out_stride, (float*)buf[4] + i * out_stride, (size_t)rows[i] * 4,
+                                      hipMemcpyDeviceToHost, c->stream),
+                       "download");
+    if (!r) r = mz_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    release();
+    return r;
 }

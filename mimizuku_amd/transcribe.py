@@ -106,6 +106,20 @@ def jump_times(w: np.ndarray, cols: int, width: int = 7, half: bool = True) -> n
     return out
 
 
+def jump_times_device(ctx, w: int, clip_stride: int, rows, cols, heads: int, cols_full: int, width: int = 7,
+                      half: bool = True) -> list[np.ndarray]:
+    """Token start times of several clips on the device (the same bits as jump_times per clip): clip c's weights are
+    rows[c] x heads x cols_full floats at device address w + 4 * c * clip_stride, cropped to cols[c] frames."""
+    rows = np.ascontiguousarray(rows, np.int32)
+    cols = np.ascontiguousarray(cols, np.int32)
+    n = len(rows)
+    stride = max(int(rows.max()) if n else 0, 1)
+    out = np.zeros((n, stride), np.float32)
+    check(L.lib().mz_jump_times_device(ctx.h, w, clip_stride, n, ptr(rows), ptr(cols), heads, cols_full, width,
+                                       int(half), ptr(out), stride))
+    return [out[c, :rows[c]] for c in range(n)]
+
+
 def dtw(m: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """DTW path (text, time indices) over cost m [rows][cols] (src/align.rs:66-106)."""
     m = np.ascontiguousarray(m, np.float64)

@@ -271,3 +271,47 @@ def test_layernorm_and_add_layernorm(ctx, dim):
     assert_f16(y, R.layer_norm((x + dlt.astype(np.float32)).astype(np.float64), w, b))
     for p in (dxx, dd, dw, db, dy):
         ctx.free(p)
+
+
+# ---------------------------------------------------------------- token timestamps (median filter + DTW)
+
+def softmax_rows(rng, shape, peak=3.0):
+    s = rng.standard_normal(shape) * peak
+    w = np.exp(s - s.max(-1, keepdims=True))
+    return (w / w.sum(-1, keepdims=True)).astype(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("half", [False, True])
+def test_timestamps_device_match_host_bits(ctx, half):
+    """k_align.hip against the host routine mz_jump_times (itself pinned to the oracle and to the golden vectors):
+    identical floats for every clip, with ragged row and column counts, clips without rows or columns, fewer
+    columns than the filter's half width, constant columns (zero deviation) and a diagonal alignment."""
+    from mimizuku_amd import transcribe
+    rng = np.random.default_rng(11 + half)
+    heads, full = 6, 1500
+    rows = [40, 1, 0, 223, 17, 5, 60, 33]
+    cols = [1500, 700, 300, 1500, 3, 0, 911, 64]
+    rmax = max(rows)
+    w = softmax_rows(rng, (len(rows), rmax, heads, full))
+    w[4, :, 2, :] = 0.25                       # constant columns in one head
+    for i in range(rows[6]):                   # a clean diagonal in clip 6
+        w[6, i, :, 15 * i:15 * i + 15] += 0.5
+    dw = ctx.upload_new(w)
+    got = transcribe.jump_times_device(ctx, dw, rmax * heads * full, rows, cols, heads, full, 7, half)
+    for c in range(len(rows)):
+        ref = transcribe.jump_times(w[c, :rows[c]], cols[c], 7, half)
+        np.testing.assert_array_equal(got[c], ref, err_msg=f"clip {c}")
+        if 0 < rows[c] <= 40 and cols[c] <= 64:
+            np.testing.assert_array_equal(got[c], R.jump_times(w[c, :rows[c]], cols[c], 7, half))
+
+
+def test_timestamps_device_other_widths(ctx):
+    from mimizuku_amd import transcribe
+    rng = np.random.default_rng(5)
+    heads, full, rows, cols = 3, 200, [12, 30], [200, 150]
+    w = softmax_rows(rng, (2, 30, heads, full))
+    dw = ctx.upload_new(w)
+    for width in (1, 5, 9, 15):
+        got = transcribe.jump_times_device(ctx, dw, 30 * heads * full, rows, cols, heads, full, width, True)
+        for c in range(2):
+            np.testing.assert_array_equal(got[c], transcribe.jump_times(w[c, :rows[c]], cols[c], width, True))
