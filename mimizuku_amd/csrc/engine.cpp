@@ -149,8 +149,8 @@ size_t weight_elems(const mz_dims& d, int* k1pad) {
 }
 
 int ksplit_for(int N, int K) {
-    // Split K over workgroups until the grid covers the 256 CUs, keeping at most 4 groups of 64 columns per wave
-    // (one batch of loads in flight) and at most MZ_MAX_PARTS partials.
+    // Split K over workgroups until the grid covers most of the 256 CUs, with at most 16 groups of 64 per workgroup
+    // (a slice within MZ_DEC_KSLICE, both operands resident in LDS) and at most MZ_MAX_PARTS partials.
     const int tiles = (N + 31) / 32, groups = K / 64;
     int best = 1;
     for (int ks = 1; ks <= std::min(groups, MZ_MAX_PARTS); ks++) {

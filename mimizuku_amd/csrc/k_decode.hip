@@ -10,12 +10,11 @@
 // every step (the reference's device-resident position, whisper.cu:7-8).
 //
 //   dec_embed_ln  token + position embedding fused with the first LayerNorm (whisper.cu:303-307, 65-69)
-//   dec_gemm      skinny GEMM for M <= 32 rows per tile on the matrix cores: W rows are the 32x32x16 MFMA A
-//                 operand, x rows the B operand; split-K over workgroups (grid.y) and over the 4 waves of a
-//                 workgroup, every wave issuing all its loads at once (the LM head two column tiles). Epilogues: fp32
-//                 split-K partials, GELU -> fp16, fp16, the self-attention q/k/v scatter into the cache, or logits
-//                 with a masked per-workgroup argmax (gemv_* + cuBLAS + fill_bias + kv_write, whisper.cu:92-97,
-//                 309-317, 497-567)
+//   dec_gemm      skinny GEMM for M <= 32 rows per tile on the matrix cores: both operands of a K slice loaded
+//                 straight into LDS at once, W rows the 32x32x16 MFMA A operand and x rows the B operand; split-K
+//                 over workgroups (grid.y) and over the 4 waves of a workgroup. Epilogues: fp32 split-K partials,
+//                 GELU -> fp16, fp16, the self-attention q/k/v scatter into the cache, or logits with a masked
+//                 per-workgroup argmax (gemv_* + cuBLAS + fill_bias + kv_write, whisper.cu:92-97, 309-317, 497-567)
 //   dec_attn      attention of one query per (row, head) over a run of keys: self-attention over the cache
 //                 (whisper.cu:319-353) and cross-attention over the encoder keys/values with the alignment-head
 //                 probabilities recorded (whisper.cu:355-449)
@@ -113,20 +112,48 @@ __global__ void __launch_bounds__(512) dec_embed_ln_kernel(const int* __restrict
 
 // ---------------------------------------------------------------- skinny GEMM
 
-// NT column tiles of 32 per wave (the LM head uses 2, so each x fragment feeds two products: the x rows, read by
-// every workgroup, are half of the traffic otherwise); DG groups of 64 columns in flight per wave. Every operand of
-// the epilogue (bias, mask, position) is requested at entry, so the kernel makes a single round trip to memory.
-template <int EPI, int NT>
+typedef __attribute__((address_space(3))) void lds_void;
+#define LDSP(q) ((lds_void*)(q))
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// One workgroup per (32 output columns, K slice, 32 rows): both operands of its K slice (<= MZ_DEC_KSLICE) go from
+// memory straight into LDS with every load issued at once (buffer_load ... lds, 16 bytes per lane), in 1 KB blocks of
+// 8 rows x 64 halves: lane i of a load writes block bytes 16 i, so one load reads 8 whole 128-byte rows (full cache
+// lines; a 32-row MFMA fragment read straight from memory touches 32 lines per instruction and runs at a quarter of
+// the rate). Block (g, rg) of an operand holds rows 8 rg .. 8 rg + 7, k = 64 g .. 64 g + 63, its row r chunk c at
+// 16-byte position c ^ r ^ (rg & 1): the fragment reads of 16 consecutive lanes (8 rows of two blocks) hit distinct
+// banks. The 4 waves split the K groups; their 32x32 products are summed in LDS. Every operand of the epilogue (bias,
+// mask, position) is requested at entry with the loads, so the kernel makes a single round trip to memory.
+template <int EPI>
 __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
-    constexpr int DG = NT == 1 ? 5 : 3;
-    constexpr int NC = 4 * NT;  // output columns per epilogue thread
-    __shared__ float red[4][32 * NT][33];
+#if defined(__HIP_DEVICE_COMPILE__)  // the buffer-resource type exists only in the device pass
+    constexpr int NC = 4;  // output columns per epilogue thread
+    __shared__ __attribute__((aligned(16))) f16 lds[64 * MZ_DEC_KSLICE];
+    f16* const sw = lds;
+    f16* const sx = lds + 32 * MZ_DEC_KSLICE;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, lh = lane >> 5;
-    const int n0 = blockIdx.x * 32 * NT, ks = blockIdx.y, m0 = blockIdx.z * 32;
-    const int gpb = (p.K >> 6) / p.ksplit, gbeg = ks * gpb;
+    const int n0 = blockIdx.x * 32, ks = blockIdx.y, m0 = blockIdx.z * 32;
+    const int ksl = p.K / p.ksplit, kb = ks * ksl, G = ksl >> 6;
     const int ml = tid >> 3, nl = (tid & 7) * NC, m = m0 + ml;
 
-    // epilogue operands first
+    // direct loads: x rows m0.., W rows n0.. (rows past M or N read zeros through the descriptor's range check)
+    const int r8 = lane >> 3, q8 = lane & 7;
+    // 32-bit offsets throughout (the operands are far below 4 GB)
+    const unsigned ldx2 = (unsigned)p.ldx * 2u, mrows = (unsigned)min(p.M - m0, 32);
+    const __amdgpu_buffer_rsrc_t rX = rsrc(p.x + (long)m0 * p.ldx, mrows * ldx2);
+    const __amdgpu_buffer_rsrc_t rW = rsrc(p.W, (unsigned)p.N * (unsigned)p.K * 2u);
+    for (int i = wave; i < 4 * G; i += 4) {
+        const int g = i >> 2, rg = i & 3, c = q8 ^ r8 ^ (rg & 1);
+        const unsigned col = (unsigned)(kb + g * 64 + c * 8) * 2;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rX, LDSP(sx + i * 512), 16, (unsigned)(rg * 8 + r8) * ldx2 + col, 0, 0,
+                                                 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, LDSP(sw + i * 512), 16,
+                                                 (unsigned)(n0 + rg * 8 + r8) * (unsigned)p.K * 2u + col, 0, 0, 0);
+    }
+    // epilogue operands
     float bv[NC];
     bool msk[NC];
 #pragma unroll
@@ -136,44 +163,26 @@ __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
         msk[e] = EPI == DEPI_LOGITS ? p.sup[n] != 0 : false;
     }
     const int pos = (EPI == DEPI_LOGITS || EPI == DEPI_QKV) ? p.ctr[1] : 0;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
 
-    const f16* wr[NT];
+    // W rows are the MFMA A operand, x rows the B operand; wave w takes K groups w, w + 4, ...
+    f32x16 acc = f32x16{};
+    const int rgx = lr >> 3, rr = lr & 7;
+    for (int g = wave; g < G; g += 4) {
+        const f16* bw = sw + (g * 4 + rgx) * 512 + rr * 64;
+        const f16* bx = sx + (g * 4 + rgx) * 512 + rr * 64;
 #pragma unroll
-    for (int t = 0; t < NT; t++) wr[t] = p.W + (long)min(n0 + 32 * t + lr, p.N - 1) * p.K + lh * 32;
-    const f16* xr = p.x + (long)min(m0 + lr, p.M - 1) * p.ldx + lh * 32;
-    f32x16 acc[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) acc[t] = f32x16{};
-    // wave w takes groups w, w + 4, w + 8, ... of the workgroup's K range, DG of them in flight at a time
-    for (int g0 = wave; g0 < gpb; g0 += 4 * DG) {
-        f16x8 wv[DG][NT][4], xv[DG][4];
-#pragma unroll
-        for (int i = 0; i < DG; i++) {
-            const int gi = g0 + 4 * i;
-            if (gi < gpb) {
-                const int k0 = (gbeg + gi) * 64;
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-#pragma unroll
-                    for (int t = 0; t < NT; t++) wv[i][t][c] = ld8(wr[t] + k0 + 8 * c);
-                    xv[i][c] = ld8(xr + k0 + 8 * c);
-                }
-            }
+        for (int st = 0; st < 4; st++) {
+            const int off = ((2 * st + lh) ^ rr ^ (rgx & 1)) << 3;
+            acc = mfma32(*(const f16x8*)(bw + off), *(const f16x8*)(bx + off), acc);
         }
-#pragma unroll
-        for (int i = 0; i < DG; i++)
-            if (g0 + 4 * i < gpb) {
-#pragma unroll
-                for (int c = 0; c < 4; c++)
-#pragma unroll
-                    for (int t = 0; t < NT; t++) acc[t] = mfma32(wv[i][t][c], xv[i][c], acc[t]);
-            }
     }
-    // accumulator r of tile t: n = n0 + 32 t + 8 (r / 4) + 4 lh + r % 4, m = m0 + lr
+    __syncthreads();  // every wave is done with the operand blocks: the LDS holds the partial products next
+    float(*red)[32][33] = (float(*)[32][33])lds;
+    // accumulator element r: n = n0 + 8 (r / 4) + 4 lh + r % 4, m = m0 + lr
 #pragma unroll
-    for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) red[wave][32 * t + 8 * (r >> 2) + 4 * lh + (r & 3)][lr] = acc[t][r];
+    for (int r = 0; r < 16; r++) red[wave][8 * (r >> 2) + 4 * lh + (r & 3)][lr] = acc[r];
     __syncthreads();
     float v[NC];
 #pragma unroll
@@ -239,6 +248,7 @@ __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
             }
         }
     }
+#endif
 }
 
 // ---------------------------------------------------------------- attention of one query per (row, head)
@@ -411,21 +421,20 @@ __global__ void __launch_bounds__(256) dec_argmax_kernel(const int2* __restrict_
 }  // namespace
 
 hipError_t mz_dec_gemm_launch(hipStream_t s, int epi, const MzDec& g) {
-    if (g.K % 64 != 0 || g.M <= 0 || g.N <= 0 || g.ksplit <= 0 || (g.K / 64) % g.ksplit != 0) return hipErrorInvalidValue;
+    if (g.K % 64 != 0 || g.M <= 0 || g.N <= 0 || g.ksplit <= 0 || (g.K / 64) % g.ksplit != 0 ||
+        g.K / g.ksplit > MZ_DEC_KSLICE || g.ldx % 8 != 0)
+        return hipErrorInvalidValue;
     if (epi == DEPI_QKV && (g.N != 3 * g.d || g.d % 64 != 0 || !g.kc || !g.vc || !g.ctr)) return hipErrorInvalidValue;
     if (epi == DEPI_LOGITS && (!g.sup || !g.amax || !g.ctr || g.M > 32)) return hipErrorInvalidValue;
     if (epi != DEPI_PARTIAL && g.ksplit != 1) return hipErrorInvalidValue;
-    dim3 grid((g.N + 31) / 32, g.ksplit, (g.M + 31) / 32);
+    static_assert(MZ_LM_COLS == 32, "one 32-column tile per workgroup");
+    const dim3 grid((g.N + 31) / 32, g.ksplit, (g.M + 31) / 32);
     switch (epi) {
-        case DEPI_PARTIAL: hipLaunchKernelGGL((dec_gemm_kernel<DEPI_PARTIAL, 1>), grid, dim3(256), 0, s, g); break;
-        case DEPI_GELU_F16: hipLaunchKernelGGL((dec_gemm_kernel<DEPI_GELU_F16, 1>), grid, dim3(256), 0, s, g); break;
-        case DEPI_QKV: hipLaunchKernelGGL((dec_gemm_kernel<DEPI_QKV, 1>), grid, dim3(256), 0, s, g); break;
-        case DEPI_F16: hipLaunchKernelGGL((dec_gemm_kernel<DEPI_F16, 1>), grid, dim3(256), 0, s, g); break;
-        case DEPI_LOGITS:
-            grid.x = (g.N + MZ_LM_COLS - 1) / MZ_LM_COLS;
-            static_assert(MZ_LM_COLS == 64, "two 32-column tiles per workgroup");
-            hipLaunchKernelGGL((dec_gemm_kernel<DEPI_LOGITS, 2>), grid, dim3(256), 0, s, g);
-            break;
+        case DEPI_PARTIAL: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_PARTIAL>, grid, dim3(256), 0, s, g); break;
+        case DEPI_GELU_F16: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_GELU_F16>, grid, dim3(256), 0, s, g); break;
+        case DEPI_QKV: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_QKV>, grid, dim3(256), 0, s, g); break;
+        case DEPI_F16: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_F16>, grid, dim3(256), 0, s, g); break;
+        case DEPI_LOGITS: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_LOGITS>, grid, dim3(256), 0, s, g); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -57,9 +57,11 @@ hipError_t mz_mel_transpose_launch(hipStream_t s, const float* mel, f16* melT, i
 // Position: ctr[0] = position of the next step; the step's first kernel (embed) copies it to ctr[1], the later
 // kernels read ctr[1], the last one (argmax) writes ctr[0] = ctr[1] + 1.
 #define MZ_MAX_PARTS 16  // split-K partials summed by dec_add_ln
-#define MZ_LM_COLS 64    // LM head columns per workgroup: one argmax partial per 64 vocabulary ids and row
+#define MZ_LM_COLS 32    // LM head columns per workgroup: one argmax partial per 32 vocabulary ids and row
+#define MZ_DEC_KSLICE 1280  // largest K slice of one skinny-GEMM workgroup (both operands resident in 160 KB of LDS)
 
-// skinny GEMM for decode batches: rows m < M of x (f16, row stride ldx, M <= 32 per m-tile) times W[N][K]
+// skinny GEMM for decode batches: rows m < M of x (f16, row stride ldx % 8 == 0, M <= 32 per m-tile) times W[N][K];
+// K / ksplit <= MZ_DEC_KSLICE
 enum MzDecEpi {
     DEPI_PARTIAL = 0,  // part[ks][m][n] (f32), ks = blockIdx.y (split-K)
     DEPI_GELU_F16 = 1, // out f16 [m][ldo] = gelu(acc + bias)
