@@ -86,7 +86,7 @@ struct mz_engine {
     float *x = nullptr, *q = nullptr, *part = nullptr, *logits = nullptr;
     f16 *h = nullptr, *datt = nullptr, *dff = nullptr, *kc = nullptr, *vc = nullptr;
     float* align = nullptr;  // alignment-head probabilities [bmax][max_t][na][1500], fp32
-    int2* amax = nullptr;  // LM head argmax partials [ceil(vocab / MZ_LM_COLS)][bmax]
+    int2* amax = nullptr;  // LM head argmax partials [mz_lm_blocks(vocab)][bmax]
     int* aslot = nullptr;
     unsigned char *sup = nullptr, *sup_lang = nullptr;
     size_t part_elems = 0;
@@ -170,7 +170,7 @@ extern "C" size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int 
     size_t enc = G * d->n_mels * NFR * 4 + G * NFR * d->n_mels * 2 + G * NFR * D * 2 + G * TENC * D * 4 +
                  G * TENC * D * 2 * 3 + G * 3 * nh * TPAD * HD * 2 + G * TENC * F * 2;
     size_t dec = B * nl * 2 * nh * TPAD * HD * 2 + B * mt * 4 + B * 4 + 16 + B * D * 4 * 2 + B * D * 2 * 2 + B * F * 2 +
-                 2 * nl * B * nh * mt * HD * 2 + B * V * 4 + B * mt * n_align * TENC * 4 + (V + MZ_LM_COLS - 1) / MZ_LM_COLS * B * 8 +
+                 2 * nl * B * nh * mt * HD * 2 + B * V * 4 + B * mt * n_align * TENC * 4 + (size_t)mz_lm_blocks((int)V) * B * 8 +
                  nl * nh * 4 + 2 * V;
     size_t part = (size_t)MZ_MAX_PARTS * B * D * 4;
     size_t ts = B * 8 + 2 * B * n_align * TENC * 4 + B * (size_t)mz_ts_diag_stride((int)mt - 1, TENC) * 5 + B * mt * 4;
@@ -316,7 +316,7 @@ extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, in
         (r = e->alloc(&e->dff, B * F)) || (r = e->alloc(&e->kc, (size_t)nl * B * nh * mt * HD)) ||
         (r = e->alloc(&e->vc, (size_t)nl * B * nh * mt * HD)) || (r = e->alloc(&e->logits, B * V)) ||
         (r = e->alloc(&e->align, B * mt * e->na * (size_t)TENC)) ||
-        (r = e->alloc(&e->amax, (size_t)((V + MZ_LM_COLS - 1) / MZ_LM_COLS) * B)) ||
+        (r = e->alloc(&e->amax, (size_t)mz_lm_blocks(V) * B)) ||
         (r = e->alloc(&e->aslot, (size_t)nl * nh)) || (r = e->alloc(&e->sup, V)) || (r = e->alloc(&e->sup_lang, V)))
         return fail(r);
     const size_t tsd = (size_t)mz_ts_diag_stride(mt - 1, TENC);
@@ -711,7 +711,7 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
         g.amax = e->amax;
         TRY(mz_dec_gemm_launch(s, DEPI_LOGITS, g), "lm head");
     }
-    TRY(mz_dec_argmax_launch(s, e->amax, (V + MZ_LM_COLS - 1) / MZ_LM_COLS, e->tok, e->done, e->ctr, b, mt, prompt_len, e->eos), "argmax");
+    TRY(mz_dec_argmax_launch(s, e->amax, mz_lm_blocks(V), e->tok, e->done, e->ctr, b, mt, prompt_len, e->eos), "argmax");
     return MZ_OK;
 }
 

@@ -117,6 +117,14 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int MZ_NT = 2;  // cache-policy bit of a buffer load: nontemporal (weights are streamed once per step)
 
+// Workgroup barrier that waits for this wave's LDS operations only, not for its loads in flight (a __syncthreads
+// would also wait for every outstanding global load); the memory clobber keeps the compiler from moving LDS
+// accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt and expcnt unconstrained
+    asm volatile("s_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigned bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
@@ -249,6 +257,154 @@ __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
                 dst[(((long)m * nh + head) * p.maxT + pos) * MZ_HD + dim] = (f16)a;
             }
         }
+    }
+#endif
+}
+
+// ---------------------------------------------------------------- LM head
+
+// Logits of <= 32 rows over the whole vocabulary, with each workgroup's masked argmax per row. The workgroup keeps
+// its rows' x in registers (the B operands of 16x16x32 products, its quarter of K per wave) and streams a contiguous
+// run of 16-column weight tiles through a 3-deep LDS ring (direct loads, two tiles in flight), so x is read once per
+// workgroup and the weight stream never waits for a round trip per tile. Ids and the argmax rules as dec_gemm's.
+constexpr int LM_TILE = 16;                          // vocabulary ids per tile
+constexpr int LM_TB = LM_TILE * MZ_DEC_KSLICE * 2;   // bytes of one weight tile in LDS
+constexpr int LM_XG = MZ_DEC_KSLICE / 64 / 4;        // K groups of 64 per wave
+
+__global__ void __launch_bounds__(256) dec_lmhead_kernel(const MzDec p, int T) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __shared__ __attribute__((aligned(16))) f16 lds[3 * LM_TB / 2 + 4 * 32 * (LM_TILE + 1) * 2];
+    float(*red)[32][LM_TILE + 1] = (float(*)[32][LM_TILE + 1])(lds + 3 * LM_TB / 2);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lq = lane >> 4;
+    const int G = p.K >> 6, ntiles = (p.N + LM_TILE - 1) / LM_TILE;
+    const int t0 = blockIdx.x * T, nt = min(T, ntiles - t0);
+    const int r8 = lane >> 3, q8 = lane & 7;
+    const int pos = p.ctr[1];
+    const bool first = pos + 1 == p.prompt_len;
+    const int em = tid >> 3, ec = (tid & 7) * 2;  // epilogue thread: row em, ids n0 + ec, n0 + ec + 1 of each tile
+    // the suppression mask of this thread's ids in every tile, requested before any other load (bit 2 t + e)
+    unsigned smask = 0;
+    {
+        unsigned char sv[32];  // all 32 byte loads in flight together (clamped ids, no branches), then combined
+#pragma unroll
+        for (int k = 0; k < 32; k++) sv[k] = p.sup[min((t0 + (k >> 1)) * LM_TILE + ec + (k & 1), p.N - 1)];
+#pragma unroll
+        for (int k = 0; k < 32; k++) {
+            const int t = k >> 1, n = (t0 + t) * LM_TILE + ec + (k & 1);
+            smask |= (t < nt && n < p.N && sv[k] ? 1u : 0u) << k;
+        }
+    }
+
+    // x rows (32 x K) through LDS into this wave's fragments: groups g = wave + 4 i, halves s of 32 k, row halves h
+    const __amdgpu_buffer_rsrc_t rX = rsrc(p.x, (unsigned)p.M * (unsigned)p.ldx * 2u);
+    for (int i = wave; i < 4 * G; i += 4) {
+        const int g = i >> 2, rg = i & 3, c = q8 ^ r8 ^ (rg & 1);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rX, LDSP(lds + i * 512), 16,
+                                                 (unsigned)(rg * 8 + r8) * (unsigned)p.ldx * 2u +
+                                                     (unsigned)(g * 64 + c * 8) * 2u,
+                                                 0, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    f16x8 xf[LM_XG][2][2];
+#pragma unroll
+    for (int i = 0; i < LM_XG; i++) {
+        const int g = wave + 4 * i;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int row = 16 * h + l16, rg = row >> 3, rr = row & 7;
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                const int c = 4 * st + lq;
+                xf[i][st][h] = g < G ? *(const f16x8*)(lds + (g * 4 + rg) * 512 + rr * 64 + ((c ^ rr ^ (rg & 1)) << 3))
+                                     : f16x8{};
+            }
+        }
+    }
+    __syncthreads();  // the x staging area becomes the weight ring
+
+    const __amdgpu_buffer_rsrc_t rW = rsrc(p.W, (unsigned)p.N * (unsigned)p.K * 2u);
+    auto issue = [&](int t) {  // tile t of this workgroup into ring slot t % 3: 2 G blocks of 8 rows x 64 k
+        f16* dst = lds + (t % 3) * (LM_TB / 2);
+        const int n0 = (t0 + t) * LM_TILE;
+        for (int i = wave; i < 2 * G; i += 4) {
+            const int g = i >> 1, rg = i & 1, c = q8 ^ r8 ^ rg;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, LDSP(dst + i * 512), 16,
+                                                     (unsigned)(n0 + rg * 8 + r8) * (unsigned)p.K * 2u +
+                                                         (unsigned)(g * 64 + c * 8) * 2u,
+                                                     0, 0, MZ_NT);
+        }
+    };
+    if (nt > 0) issue(0);
+    if (nt > 1) issue(1);
+
+    // running best of this thread's row over the workgroup's tiles
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int t = 0; t < nt; t++) {
+        // tile t landed (at most the next tile's loads, issued after it, still in flight); every wave is done with
+        // the slot the next issue overwrites and with the previous tile's partial sums
+        // (the count is exact for K = MZ_DEC_KSLICE: 10 weight loads per wave per tile; loads complete in order, so
+        // with 10 or fewer operations outstanding none of tile t's loads is)
+        static_assert(2 * MZ_DEC_KSLICE / 64 / 4 == 10, "10 weight loads per wave per tile at the full K");
+        if (t + 1 < nt && G == MZ_DEC_KSLICE / 64)
+            __builtin_amdgcn_s_waitcnt((10 & 15) | (7 << 4) | (15 << 8));
+        else
+            __builtin_amdgcn_s_waitcnt(0);
+        lds_barrier();
+        if (t + 2 < nt) issue(t + 2);
+        const f16* wt = lds + (t % 3) * (LM_TB / 2);
+        f32x4 acc0 = f32x4{}, acc1 = f32x4{};
+        const int rg = l16 >> 3, rr = l16 & 7;
+#pragma unroll
+        for (int i = 0; i < LM_XG; i++) {
+            const int g = wave + 4 * i;
+            if (g < G) {
+#pragma unroll
+                for (int st = 0; st < 2; st++) {
+                    const int c = 4 * st + lq;
+                    const f16x8 wf = *(const f16x8*)(wt + (g * 2 + rg) * 512 + rr * 64 + ((c ^ rr ^ rg) << 3));
+                    acc0 = mfma16(wf, xf[i][st][0], acc0);
+                    acc1 = mfma16(wf, xf[i][st][1], acc1);
+                }
+            }
+        }
+        // element r of lane l: id n0 + 4 (l / 16) + r, row l % 16 (+ 16 for acc1)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            red[wave][l16][4 * lq + r] = acc0[r];
+            red[wave][16 + l16][4 * lq + r] = acc1[r];
+        }
+        lds_barrier();
+        const int n0 = (t0 + t) * LM_TILE;
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int n = n0 + ec + e;
+            const float v = red[0][em][ec + e] + red[1][em][ec + e] + red[2][em][ec + e] + red[3][em][ec + e];
+            if (em < p.M && n < p.N) {
+                ((float*)p.out)[(long)em * p.ldo + n] = v;
+                const bool masked = ((smask >> (2 * t + e)) & 1u) || (first && (n == p.bs1 || n == p.bs2));
+                if (!masked && (v > best || (v == best && n < bi))) {
+                    best = v;
+                    bi = n;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {  // the 8 threads of one row are adjacent lanes
+        const float ov = __shfl_xor(best, o);
+        const int oi = __shfl_xor(bi, o);
+        if (ov > best || (ov == best && oi < bi)) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    if ((tid & 7) == 0 && em < p.M) {
+        int2 r;
+        r.x = __float_as_int(best);
+        r.y = bi;
+        ((int2*)p.amax)[(long)blockIdx.x * p.M + em] = r;
     }
 #endif
 }
@@ -423,21 +579,33 @@ __global__ void __launch_bounds__(256) dec_argmax_kernel(const int2* __restrict_
 
 }  // namespace
 
+int mz_lm_tiles_per_block(int N) {
+    const int ntiles = (N + LM_TILE - 1) / LM_TILE;
+    return (ntiles + 255) / 256;  // at most 16 for N <= 65536 (the per-thread mask holds 2 bits per tile)
+}
+int mz_lm_blocks(int N) {
+    const int ntiles = (N + LM_TILE - 1) / LM_TILE, T = mz_lm_tiles_per_block(N);
+    return (ntiles + T - 1) / T;
+}
+
 hipError_t mz_dec_gemm_launch(hipStream_t s, int epi, const MzDec& g) {
     if (g.K % 64 != 0 || g.M <= 0 || g.N <= 0 || g.ksplit <= 0 || (g.K / 64) % g.ksplit != 0 ||
         g.K / g.ksplit > MZ_DEC_KSLICE || g.ldx % 8 != 0)
         return hipErrorInvalidValue;
     if (epi == DEPI_QKV && (g.N != 3 * g.d || g.d % 64 != 0 || !g.kc || !g.vc || !g.ctr)) return hipErrorInvalidValue;
-    if (epi == DEPI_LOGITS && (!g.sup || !g.amax || !g.ctr || g.M > 32)) return hipErrorInvalidValue;
+    if (epi == DEPI_LOGITS && (!g.sup || !g.amax || !g.ctr || g.M > 32 || g.N > 65536)) return hipErrorInvalidValue;
     if (epi != DEPI_PARTIAL && g.ksplit != 1) return hipErrorInvalidValue;
-    static_assert(MZ_LM_COLS == 32, "one 32-column tile per workgroup");
     const dim3 grid((g.N + 31) / 32, g.ksplit, (g.M + 31) / 32);
     switch (epi) {
         case DEPI_PARTIAL: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_PARTIAL>, grid, dim3(256), 0, s, g); break;
         case DEPI_GELU_F16: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_GELU_F16>, grid, dim3(256), 0, s, g); break;
         case DEPI_QKV: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_QKV>, grid, dim3(256), 0, s, g); break;
         case DEPI_F16: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_F16>, grid, dim3(256), 0, s, g); break;
-        case DEPI_LOGITS: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_LOGITS>, grid, dim3(256), 0, s, g); break;
+        case DEPI_LOGITS: {
+            const int T = mz_lm_tiles_per_block(g.N);
+            hipLaunchKernelGGL(dec_lmhead_kernel, dim3(mz_lm_blocks(g.N)), dim3(256), 0, s, g, T);
+            break;
+        }
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -57,7 +57,6 @@ hipError_t mz_mel_transpose_launch(hipStream_t s, const float* mel, f16* melT, i
 // Position: ctr[0] = position of the next step; the step's first kernel (embed) copies it to ctr[1], the later
 // kernels read ctr[1], the last one (argmax) writes ctr[0] = ctr[1] + 1.
 #define MZ_MAX_PARTS 16  // split-K partials summed by dec_add_ln
-#define MZ_LM_COLS 32    // LM head columns per workgroup: one argmax partial per 32 vocabulary ids and row
 #define MZ_DEC_KSLICE 1280  // largest K slice of one skinny-GEMM workgroup (both operands resident in 160 KB of LDS)
 
 // skinny GEMM for decode batches: rows m < M of x (f16, row stride ldx % 8 == 0, M <= 32 per m-tile) times W[N][K];
@@ -65,7 +64,8 @@ hipError_t mz_mel_transpose_launch(hipStream_t s, const float* mel, f16* melT, i
 enum MzDecEpi {
     DEPI_PARTIAL = 0,  // part[ks][m][n] (f32), ks = blockIdx.y (split-K)
     DEPI_GELU_F16 = 1, // out f16 [m][ldo] = gelu(acc + bias)
-    DEPI_LOGITS = 2,   // out f32 [m][ldo] = acc, and amax[blockIdx.x][m] = masked (max, lowest id) of the 32 columns
+    DEPI_LOGITS = 2,   // out f32 [m][ldo] = acc, and amax[wg][m] = masked (max, lowest id) of each workgroup's ids
+                       // (mz_lm_blocks(N) workgroups; M <= 32, K <= MZ_DEC_KSLICE)
     DEPI_QKV = 3,      // q -> out f32 [m][d] (+bias); k, v (+bias) -> self cache rows at position ctr[1]
     DEPI_F16 = 4,      // out f16 [m][ldo] = acc + bias
 };
@@ -85,9 +85,12 @@ struct MzDec {
     // DEPI_LOGITS: mask (nonzero = never chosen), begin-suppressed ids at the first generated position, partials
     const unsigned char* sup;
     int bs1, bs2, prompt_len;
-    void* amax;  // int2 {float bits, id} [ceil(N / MZ_LM_COLS)][M]
+    void* amax;  // int2 {float bits, id} [mz_lm_blocks(N)][M]
 };
 hipError_t mz_dec_gemm_launch(hipStream_t s, int epi, const MzDec& g);
+// LM head workgroups (each with one argmax partial per row) and vocabulary tiles of 16 per workgroup
+int mz_lm_blocks(int N);
+int mz_lm_tiles_per_block(int N);
 
 struct MzDecAttn {
     // query: sum over nq slices of q[s * qstride + b * d + head * 64 + i] (+ qbias), scaled by 1/8
