@@ -4,11 +4,19 @@
 //
 // Work: one block per (256 queries, head, clip) = 4 waves x 2 sets of 32 queries. K and V^T tiles of 64 keys are
 // staged in LDS (double buffered, register prefetch) and shared by the 4 waves. Scores are computed transposed,
-// S^T = K Q^T (32x32x16 MFMA), so each lane owns one query column: the running max / sum and the rescale of O are
-// per lane, and the only cross-lane step is one swap with lane l ^ 32. K rows are stored in LDS with bits 2 and 3
-// of the key index swapped, which makes each lane's 16 scores two runs of 8 consecutive keys: the scores, rounded
-// to fp16, are directly the B operand of O^T = V^T P^T, and V^T (written transposed by the QKV GEMM) is read with
-// 16-byte LDS loads. exp uses v_exp_f32 (exp2) with log2(e) folded into the scale.
+// S^T = K Q^T (32x32x16 MFMA), so each lane owns one query column: the running max and the rescale of O are per
+// lane, and the only cross-lane step is one swap with lane l ^ 32. K rows are stored in LDS with bits 2 and 3 of the
+// key index swapped, which makes each lane's 16 scores two runs of 8 consecutive keys: the probabilities, rounded to
+// fp16, are directly the B operand of O^T = V^T P^T, and V^T (written transposed by the QKV GEMM) is read with
+// 16-byte LDS loads.
+//
+// On this part the vector ALU and the matrix cores of a SIMD do not overlap (an MFMA and the vector instructions
+// around it take the sum of their times), so every vector instruction per score counts: the running max is raised
+// only when a block's scores exceed it by more than 2^8 (p = exp2(s - m) <= 256 is exact enough in fp16 and keeps
+// the rescale of O rare), the row sums add the fp16 probabilities two per dot2 instruction, and the key mask of the
+// padded last tile is applied in that tile only.
+#include <type_traits>
+
 #include "mz_common.h"
 #include "mz_kernels.h"
 
@@ -38,6 +46,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int d = nh * MZ_HD;
 
     // query fragments (B operand of S^T): query row, dims 16c + 8 lh .. + 8
+    const float cs = 0.125f * 1.4426950408889634f;  // scale * log2(e)
     const int q0 = qb * QB + wave * 64;
     f16x8 qf[2][4];
 #pragma unroll
@@ -62,8 +71,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         *(f16x8*)&sV[buf][kr1 * KP + cc] = pv1;
     };
 
-    const float cs = 0.125f * 1.4426950408889634f;  // scale * log2(e)
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+    constexpr float TAU = 8.f;  // log2 of the largest unnormalised probability before O is rescaled
+    float m[2] = {0.f, 0.f};    // running max of the scaled scores (per query column); set by the first block
+    float l[2] = {0.f, 0.f};
     f32x16 o[2][2];
 #pragma unroll
     for (int s = 0; s < 2; s++) o[s][0] = o[s][1] = f32x16{};
@@ -71,9 +81,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     gload(0);
     lstore(0);
     __syncthreads();
-    for (int kt = 0; kt < NT; kt++) {
+    // one 64-key tile; LAST masks the keys past 1500 of the padded last tile
+    auto tile = [&](int kt, auto last) {
+        constexpr bool LAST = decltype(last)::value;
         const int buf = kt & 1;
-        if (kt + 1 < NT) gload(kt + 1);
+        if (!LAST) gload(kt + 1);
 #pragma unroll
         for (int ss = 0; ss < 2; ss++) {  // 32-key halves of the tile
             f16x8 kf[4], vf[2][2];
@@ -89,45 +101,49 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                 f32x16 sc = {};
 #pragma unroll
                 for (int c = 0; c < 4; c++) sc = mfma32(kf[c], qf[qs][c], sc);
-                if (kt == NT - 1) {
+                if (LAST) {
 #pragma unroll
                     for (int r = 0; r < 16; r++) {
-                        int key = kt * 64 + 32 * ss + 16 * (r >> 3) + 8 * lh + (r & 7);
+                        const int key = kt * 64 + 32 * ss + 16 * (r >> 3) + 8 * lh + (r & 7);
                         if (key >= MZ_TENC) sc[r] = -INFINITY;
                     }
                 }
-                float mx = sc[0];
+                float mx = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
 #pragma unroll
-                for (int r = 1; r < 16; r++) mx = fmaxf(mx, sc[r]);
-                mx = fmaxf(mx, __shfl_xor(mx, 32));
-                const float mnew = fmaxf(m[qs], mx * cs);
-                const float corr = __builtin_amdgcn_exp2f(m[qs] - mnew);
-                m[qs] = mnew;
-                l[qs] *= corr;
-                if (__ballot(corr != 1.f)) {
+                for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sc[r]), sc[r + 1]);
+                mx = fmaxf(mx, sc[15]);
+                mx = fmaxf(mx, __shfl_xor(mx, 32)) * cs - m[qs];  // block max over the running max
+                // first block: the max becomes this block's max; later: raised only past TAU (wave-uniform branch)
+                const bool first = kt == 0 && ss == 0;
+                if (__ballot(first || mx > TAU)) {
+                    const float dm = (first || mx > TAU) ? mx : 0.f;
+                    const float corr = __builtin_amdgcn_exp2f(-dm);
+                    m[qs] += dm;
+                    l[qs] *= corr;
 #pragma unroll
                     for (int t = 0; t < 2; t++)
 #pragma unroll
                         for (int r = 0; r < 16; r++) o[qs][t][r] *= corr;
                 }
                 f16x8 pf[2];
-                float ls = 0.f;
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    float pr = __builtin_amdgcn_exp2f(fmaf(sc[r], cs, -mnew));
-                    ls += pr;
-                    pf[r >> 3][r & 7] = (f16)pr;
-                }
-                l[qs] += ls;
+                for (int r = 0; r < 16; r++) pf[r >> 3][r & 7] = (f16)__builtin_amdgcn_exp2f(fmaf(sc[r], cs, -m[qs]));
+                // row sum of the fp16 probabilities (the ones that weight V), two per dot2 with fp32 accumulation
+#pragma unroll
+                for (int r = 0; r < 16; r += 2)
+                    l[qs] = __builtin_amdgcn_fdot2(f16x2{pf[r >> 3][r & 7], pf[r >> 3][(r & 7) + 1]}, f16x2{1, 1}, l[qs],
+                                                   false);
 #pragma unroll
                 for (int t = 0; t < 2; t++)
 #pragma unroll
                     for (int c = 0; c < 2; c++) o[qs][t] = mfma32(vf[t][c], pf[c], o[qs][t]);
             }
         }
-        if (kt + 1 < NT) lstore(buf ^ 1);
+        if (!LAST) lstore(buf ^ 1);
         __syncthreads();
-    }
+    };
+    for (int kt = 0; kt < NT - 1; kt++) tile(kt, std::false_type{});
+    tile(NT - 1, std::true_type{});
 
 #pragma unroll
     for (int qs = 0; qs < 2; qs++) {

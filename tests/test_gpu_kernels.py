@@ -1,8 +1,9 @@
 """GPU parity of the individual kernels through the C ABI, against float64 closed forms on the same fp16 inputs (or
 the oracle's functions), at small shapes and at the full large-v3 shapes with subsampled checks.
 
-Tolerances: an fp16 output is the exact result rounded to fp16 within one ulp (assert_f16); an fp32 output, and the
-attention output (whose P operand the kernel rounds to fp16), within max-abs error <= 2e-3 x RMS of the reference.
+Tolerances: an fp16 output is the exact result rounded to fp16 within one ulp (assert_f16); an fp32 output within
+max-abs error <= 2e-3 x RMS of the reference; the attention output (whose P operand the kernel rounds to fp16) within
+the larger of that and 1.5 x the error of the same attention computed exactly but with fp16 probabilities.
 """
 import numpy as np
 import pytest
@@ -77,12 +78,27 @@ def attention64(q, k, v):
     return R.attention(q, k, v, 0.125, dtype=np.float64)
 
 
+def attention_p16(q, k, v):
+    """The fp16-probability arithmetic the kernel (and the reference's fused attention) uses, otherwise exact:
+    P = fp16(exp(s - max)), O = fp16(P v / sum P)."""
+    s = (q.astype(np.float64) * 0.125) @ np.swapaxes(k.astype(np.float64), -1, -2)
+    p = np.exp(s - s.max(-1, keepdims=True)).astype(np.float16).astype(np.float64)
+    return ((p @ v.astype(np.float64)) / p.sum(-1, keepdims=True)).astype(np.float16)
+
+
+def attention_bar(q, k, v, ref):
+    """Error bar of an fp16-probability attention: the larger of TOL and 1.5 x the error of attention_p16, whose fp16
+    rounding of P and of the output alone reaches about 2e-3 x RMS on near-uniform softmaxes. The max-abs metric
+    moves by about +-25% with where the running max stands when each P is rounded (blockwise vs exact max)."""
+    return max(TOL, 1.5 * rel_err(attention_p16(q, k, v), ref))
+
+
 def test_enc_attention_small(ctx):
     rng = np.random.default_rng(10)
     q, k, v = (f16(rng, (1, 2, 1500, 64)) for _ in range(3))
     out = run_attention(ctx, q, k, v)
     ref = attention64(q, k, v)
-    assert rel_err(out, ref) < TOL
+    assert rel_err(out, ref) < attention_bar(q, k, v, ref)
     # a transposed V (a plausible layout mistake) is far outside the bar
     assert rel_err(out, attention64(q, k, v[..., ::-1])) > 0.1
 
@@ -93,7 +109,8 @@ def test_enc_attention_peaked_scores(ctx):
     q, k = f16(rng, (1, 1, 1500, 64), 4.0), f16(rng, (1, 1, 1500, 64), 4.0)
     v = f16(rng, (1, 1, 1500, 64))
     out = run_attention(ctx, q, k, v)
-    assert rel_err(out, attention64(q, k, v)) < TOL
+    ref = attention64(q, k, v)
+    assert rel_err(out, ref) < attention_bar(q, k, v, ref)
 
 
 def test_enc_attention_large_v3_shape(ctx):
@@ -105,7 +122,7 @@ def test_enc_attention_large_v3_shape(ctx):
     out = run_attention(ctx, q, k, v)
     rows = np.r_[np.arange(0, 1500, 37), 1496, 1497, 1498, 1499]
     ref = attention64(q[:, :, rows], k, v)
-    assert rel_err(out[:, :, rows], ref) < TOL
+    assert rel_err(out[:, :, rows], ref) < attention_bar(q[:, :, rows], k, v, ref)
     assert np.isfinite(out).all()
 
 
