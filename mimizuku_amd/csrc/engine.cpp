@@ -52,6 +52,12 @@ inline int rup(int x, int m) { return (x + m - 1) / m * m; }
 
 }  // namespace
 
+struct EncBufs {
+    float* mel;
+    f16 *melT, *h1, *hb, *qkvh, *att, *ff, *dd;
+    float* ex;
+};
+
 struct mz_engine {
     mz_ctx* c = nullptr;
     mz_dims dm{};
@@ -80,6 +86,11 @@ struct mz_engine {
     f16 *melT = nullptr, *h1 = nullptr, *hb = nullptr, *qkvh = nullptr, *att = nullptr, *ff = nullptr;
     f16* dd = nullptr;  // out-projection / fc2 output, added to the residual stream by the next add + LayerNorm
     float *ex = nullptr, *trace = nullptr;
+    // a second encoder lane for batches of several groups: its own scratch and stream, so that one group's
+    // bandwidth-bound kernels and kernel tails overlap the other's products (the groups are independent)
+    EncBufs lane1{};
+    hipStream_t s2 = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
     // decoder state (bmax rows)
     f16* xkvbuf = nullptr;
     int *tok = nullptr, *done = nullptr, *ctr = nullptr;
@@ -174,7 +185,7 @@ extern "C" size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int 
                  nl * nh * 4 + 2 * V;
     size_t part = (size_t)MZ_MAX_PARTS * B * D * 4;
     size_t ts = B * 8 + 2 * B * n_align * TENC * 4 + B * (size_t)mz_ts_diag_stride((int)mt - 1, TENC) * 5 + B * mt * 4;
-    return enc + dec + part + ts;
+    return 2 * enc + dec + part + ts;  // two encoder lanes
 }
 
 extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, int bmax, int eg, mz_engine** out) {
@@ -310,6 +321,20 @@ extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, in
         (r = e->alloc(&e->att, G * TENC * D)) || (r = e->alloc(&e->ff, G * TENC * F)) ||
         (r = e->alloc(&e->dd, G * TENC * D)))
         return fail(r);
+    {
+        EncBufs& l = e->lane1;
+        if ((r = e->alloc(&l.mel, G * d->n_mels * NFR)) || (r = e->alloc(&l.melT, G * NFR * d->n_mels)) ||
+            (r = e->alloc(&l.h1, G * NFR * D)) || (r = e->alloc(&l.ex, G * TENC * D)) ||
+            (r = e->alloc(&l.hb, G * TENC * D)) || (r = e->alloc(&l.qkvh, G * 3 * nh * (size_t)TPAD * HD)) ||
+            (r = e->alloc(&l.att, G * TENC * D)) || (r = e->alloc(&l.ff, G * TENC * F)) ||
+            (r = e->alloc(&l.dd, G * TENC * D)))
+            return fail(r);
+        // default priority (as the context's stream)
+        if ((r = mz_hip(hipStreamCreateWithFlags(&e->s2, hipStreamNonBlocking), "hipStreamCreate")) ||
+            (r = mz_hip(hipEventCreateWithFlags(&e->fork, hipEventDisableTiming), "hipEventCreate")) ||
+            (r = mz_hip(hipEventCreateWithFlags(&e->join, hipEventDisableTiming), "hipEventCreate")))
+            return fail(r);
+    }
     if ((r = e->alloc(&e->xkvbuf, B * nl * 2 * nh * (size_t)TPAD * HD)) || (r = e->alloc(&e->tok, B * mt)) ||
         (r = e->alloc(&e->done, B)) || (r = e->alloc(&e->ctr, 4)) || (r = e->alloc(&e->x, B * D)) ||
         (r = e->alloc(&e->q, B * D)) || (r = e->alloc(&e->h, B * D)) || (r = e->alloc(&e->datt, B * D)) ||
@@ -426,23 +451,25 @@ extern "C" int mz_engine_set_trace(mz_engine* e, int on) {
         }                                                                           \
     } while (0)
 
-static int encode_impl(mz_engine* e, const float* mels, bool on_device, int n, int slot0) {
+static int encode_impl(mz_engine* e, const float* mels, bool on_device, int n, int slot0, int lane = 0) {
     if (!e || !mels) return mz_fail(MZ_ERR_ARG, "mz_engine_encode: null argument");
     if (!e->loaded) return mz_fail(MZ_ERR_STATE, "mz_engine_encode: weights not loaded (mz_engine_finish)");
     if (n <= 0 || n > e->eg || slot0 < 0 || slot0 + n > e->bmax)
         return mz_fail(MZ_ERR_ARG, "mz_engine_encode: %d clips at slot %d (enc group %d, bmax %d)", n, slot0, e->eg, e->bmax);
-    hipStream_t s = e->c->stream;
+    if (lane && e->trace_on) return mz_fail(MZ_ERR_STATE, "encoder trace on the second lane");
+    hipStream_t s = lane ? e->s2 : e->c->stream;
+    const EncBufs B = lane ? e->lane1 : EncBufs{e->mel, e->melT, e->h1, e->hb, e->qkvh, e->att, e->ff, e->dd, e->ex};
     const int D = e->dm.d, nm = e->dm.n_mels, nh = e->dm.nh, F = e->dm.ff, nl = e->dm.dec_layers;
     const int rows = n * TENC;
     const float* src = mels;
     if (!on_device) {
-        TRY(hipMemcpyAsync(e->mel, mels, (size_t)n * nm * NFR * 4, hipMemcpyHostToDevice, s), "mel upload");
-        src = e->mel;
+        TRY(hipMemcpyAsync(B.mel, mels, (size_t)n * nm * NFR * 4, hipMemcpyHostToDevice, s), "mel upload");
+        src = B.mel;
     }
-    PROF(MZ_K_MEL, mz_mel_transpose_launch(s, src, e->melT, n, nm), "mel transpose");
+    PROF(MZ_K_MEL, mz_mel_transpose_launch(s, src, B.melT, n, nm), "mel transpose");
     // conv stem as implicit GEMMs (src/model.rs:552-558): GELU(conv1), GELU(conv2, stride 2) + positions
     MzGemm g{};
-    g.A = e->melT;
+    g.A = B.melT;
     g.W = e->conv1.w;
     g.bias = e->conv1.b;
     g.M = n * NFR;
@@ -452,11 +479,11 @@ static int encode_impl(mz_engine* e, const float* mels, bool on_device, int n, i
     g.conv_tin = NFR;
     g.conv_tout = NFR;
     g.conv_stride = 1;
-    g.out = e->h1;
+    g.out = B.h1;
     g.ldo = D;
     PROF(MZ_K_CONV1, mz_gemm_launch(s, ALOAD_CONV, EPI_GELU_F16, g), "conv1");
     g = MzGemm{};
-    g.A = e->h1;
+    g.A = B.h1;
     g.W = e->conv2.w;
     g.bias = e->conv2.b;
     g.M = rows;
@@ -466,67 +493,67 @@ static int encode_impl(mz_engine* e, const float* mels, bool on_device, int n, i
     g.conv_tin = NFR;
     g.conv_tout = TENC;
     g.conv_stride = 2;
-    g.out = e->ex;
+    g.out = B.ex;
     g.ldo = D;
     g.pos = e->epos;
     PROF(MZ_K_CONV2, mz_gemm_launch(s, ALOAD_CONV, EPI_GELU_POS, g), "conv2");
-    PROF(MZ_K_LN, mz_layernorm_launch(s, e->ex, D, e->encv[0].ln1.w, e->encv[0].ln1.b, e->hb, D, rows, D, EPS), "ln");
+    PROF(MZ_K_LN, mz_layernorm_launch(s, B.ex, D, e->encv[0].ln1.w, e->encv[0].ln1.b, B.hb, D, rows, D, EPS), "ln");
     for (int i = 0; i < e->dm.enc_layers; i++) {
         const EncLayer& L = e->encv[i];
         if (e->trace_on)
-            TRY(hipMemcpyAsync(e->trace + (size_t)i * e->eg * TENC * D, e->ex, (size_t)rows * D * 4,
+            TRY(hipMemcpyAsync(e->trace + (size_t)i * e->eg * TENC * D, B.ex, (size_t)rows * D * 4,
                                hipMemcpyDeviceToDevice, s),
                 "trace");
         g = MzGemm{};
-        g.A = e->hb;
+        g.A = B.hb;
         g.lda = D;
         g.W = L.qkv.w;
         g.bias = L.qkv.b;
         g.M = rows;
         g.N = 3 * D;
         g.K = D;
-        g.heads = e->qkvh;
+        g.heads = B.qkvh;
         g.blocks_per_clip = 3 * nh;
         g.nh = nh;
         g.kind = 3;
         PROF(MZ_K_QKV, mz_gemm_launch(s, ALOAD_PLAIN, EPI_HEADS, g), "qkv");
-        PROF(MZ_K_ATTN, mz_enc_attention_launch(s, e->qkvh, e->att, n, nh), "attention");
+        PROF(MZ_K_ATTN, mz_enc_attention_launch(s, B.qkvh, B.att, n, nh), "attention");
         g = MzGemm{};
-        g.A = e->att;
+        g.A = B.att;
         g.lda = D;
         g.W = L.o.w;
         g.bias = L.o.b;
         g.M = rows;
         g.N = D;
         g.K = D;
-        g.out = e->dd;
+        g.out = B.dd;
         g.ldo = D;
         // the projection's output is rounded to fp16 once (as the reference's linear outputs) and added to the fp32
         // residual stream by the streaming add + LayerNorm, which also normalises for fc1
         PROF(MZ_K_OPROJ, mz_gemm_launch(s, ALOAD_PLAIN, EPI_F16, g), "out-proj");
-        PROF(MZ_K_LN, mz_add_layernorm_launch(s, e->ex, e->dd, L.ln2.w, L.ln2.b, e->hb, rows, D, EPS), "add+ln2");
-        g.A = e->hb;
+        PROF(MZ_K_LN, mz_add_layernorm_launch(s, B.ex, B.dd, L.ln2.w, L.ln2.b, B.hb, rows, D, EPS), "add+ln2");
+        g.A = B.hb;
         g.W = L.fc1.w;
         g.bias = L.fc1.b;
         g.N = F;
-        g.out = e->ff;
+        g.out = B.ff;
         g.ldo = F;
         PROF(MZ_K_FC1, mz_gemm_launch(s, ALOAD_PLAIN, EPI_GELU_F16, g), "fc1");
-        g.A = e->ff;
+        g.A = B.ff;
         g.lda = F;
         g.W = L.fc2.w;
         g.bias = L.fc2.b;
         g.N = D;
         g.K = F;
-        g.out = e->dd;
+        g.out = B.dd;
         g.ldo = D;
         PROF(MZ_K_FC2, mz_gemm_launch(s, ALOAD_PLAIN, EPI_F16, g), "fc2");
         const Ln& nx = i + 1 < e->dm.enc_layers ? e->encv[i + 1].ln1 : e->eln;  // the last one is the final LN
-        PROF(MZ_K_LN, mz_add_layernorm_launch(s, e->ex, e->dd, nx.w, nx.b, e->hb, rows, D, EPS), "add+ln");
+        PROF(MZ_K_LN, mz_add_layernorm_launch(s, B.ex, B.dd, nx.w, nx.b, B.hb, rows, D, EPS), "add+ln");
     }
     // cross k/v of every decoder layer for the clips' slots (src/model.rs:614-623)
     g = MzGemm{};
-    g.A = e->hb;
+    g.A = B.hb;
     g.lda = D;
     g.W = e->xkv.w;
     g.bias = e->xkv.b;
@@ -810,6 +837,17 @@ extern "C" int mz_engine_free(mz_engine* e) {
         hipEventDestroy(r.b);
     }
     for (hipEvent_t x : e->evpool) hipEventDestroy(x);
+    if (e->s2) {
+        hipStreamSynchronize(e->s2);
+        hipStreamDestroy(e->s2);
+    }
+    if (e->fork) hipEventDestroy(e->fork);
+    if (e->join) hipEventDestroy(e->join);
+    const EncBufs& l = e->lane1;
+    for (void* p : {(void*)l.mel, (void*)l.melT, (void*)l.h1, (void*)l.hb, (void*)l.qkvh, (void*)l.att, (void*)l.ff,
+                    (void*)l.dd, (void*)l.ex, (void*)e->ts_rc, (void*)e->ts_mean, (void*)e->ts_sd, (void*)e->ts_cost,
+                    (void*)e->ts_trace, (void*)e->ts_out})
+        if (p) mz_free(e->c, (uint64_t)(uintptr_t)p);
     for (void* p : {(void*)e->arena, (void*)e->mel, (void*)e->melT, (void*)e->h1, (void*)e->ex, (void*)e->hb, (void*)e->dd,
                     (void*)e->qkvh, (void*)e->att, (void*)e->ff, (void*)e->trace, (void*)e->xkvbuf, (void*)e->tok,
                     (void*)e->done, (void*)e->ctr, (void*)e->x, (void*)e->q, (void*)e->h, (void*)e->datt,
@@ -839,9 +877,20 @@ static int transcribe_impl(mz_engine* e, const float* mels, bool on_device, cons
     mz_times tm{};
 
     auto t0 = clk::now();
-    for (int g0 = 0; g0 < n; g0 += e->eg) {
+    // groups alternate between the two encoder lanes (the second waits for the caller's work on the main stream,
+    // the main stream for the second before decoding)
+    const bool two = n > e->eg && !e->trace_on;
+    if (two) {
+        TRY(hipEventRecord(e->fork, e->c->stream), "hipEventRecord");
+        TRY(hipStreamWaitEvent(e->s2, e->fork, 0), "hipStreamWaitEvent");
+    }
+    for (int g0 = 0, gi = 0; g0 < n; g0 += e->eg, gi++) {
         const int gn = std::min(e->eg, n - g0);
-        if (int r = encode_impl(e, mels + (size_t)g0 * nm * NFR, on_device, gn, g0)) return r;
+        if (int r = encode_impl(e, mels + (size_t)g0 * nm * NFR, on_device, gn, g0, two ? gi & 1 : 0)) return r;
+    }
+    if (two) {
+        TRY(hipEventRecord(e->join, e->s2), "hipEventRecord");
+        TRY(hipStreamWaitEvent(e->c->stream, e->join, 0), "hipStreamWaitEvent");
     }
     if (int r = mz_sync(e->c)) return r;
     tm.enc = sec(t0);
