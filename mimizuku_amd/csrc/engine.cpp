@@ -52,6 +52,10 @@ inline int rup(int x, int m) { return (x + m - 1) / m * m; }
 
 }  // namespace
 
+#ifndef MZ_ENC_LANES
+#define MZ_ENC_LANES 2  // encoder groups in flight at once in mz_transcribe
+#endif
+
 struct EncBufs {
     float* mel;
     f16 *melT, *h1, *hb, *qkvh, *att, *ff, *dd;
@@ -86,11 +90,11 @@ struct mz_engine {
     f16 *melT = nullptr, *h1 = nullptr, *hb = nullptr, *qkvh = nullptr, *att = nullptr, *ff = nullptr;
     f16* dd = nullptr;  // out-projection / fc2 output, added to the residual stream by the next add + LayerNorm
     float *ex = nullptr, *trace = nullptr;
-    // a second encoder lane for batches of several groups: its own scratch and stream, so that one group's
-    // bandwidth-bound kernels and kernel tails overlap the other's products (the groups are independent)
-    EncBufs lane1{};
-    hipStream_t s2 = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr;
+    // more encoder lanes for batches of several groups: each with its own scratch and stream, so that one group's
+    // bandwidth-bound kernels and kernel tails overlap another's products (the groups are independent)
+    EncBufs lanes[MZ_ENC_LANES - 1]{};
+    hipStream_t ls[MZ_ENC_LANES - 1]{};
+    hipEvent_t fork = nullptr, join[MZ_ENC_LANES - 1]{};
     // decoder state (bmax rows)
     f16* xkvbuf = nullptr;
     int *tok = nullptr, *done = nullptr, *ctr = nullptr;
@@ -185,7 +189,7 @@ extern "C" size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int 
                  nl * nh * 4 + 2 * V;
     size_t part = (size_t)MZ_MAX_PARTS * B * D * 4;
     size_t ts = B * 8 + 2 * B * n_align * TENC * 4 + B * (size_t)mz_ts_diag_stride((int)mt - 1, TENC) * 5 + B * mt * 4;
-    return 2 * enc + dec + part + ts;  // two encoder lanes
+    return MZ_ENC_LANES * enc + dec + part + ts;
 }
 
 extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, int bmax, int eg, mz_engine** out) {
@@ -321,8 +325,9 @@ extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, in
         (r = e->alloc(&e->att, G * TENC * D)) || (r = e->alloc(&e->ff, G * TENC * F)) ||
         (r = e->alloc(&e->dd, G * TENC * D)))
         return fail(r);
-    {
-        EncBufs& l = e->lane1;
+    if ((r = mz_hip(hipEventCreateWithFlags(&e->fork, hipEventDisableTiming), "hipEventCreate"))) return fail(r);
+    for (int k = 0; k < MZ_ENC_LANES - 1; k++) {
+        EncBufs& l = e->lanes[k];
         if ((r = e->alloc(&l.mel, G * d->n_mels * NFR)) || (r = e->alloc(&l.melT, G * NFR * d->n_mels)) ||
             (r = e->alloc(&l.h1, G * NFR * D)) || (r = e->alloc(&l.ex, G * TENC * D)) ||
             (r = e->alloc(&l.hb, G * TENC * D)) || (r = e->alloc(&l.qkvh, G * 3 * nh * (size_t)TPAD * HD)) ||
@@ -330,9 +335,8 @@ extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, in
             (r = e->alloc(&l.dd, G * TENC * D)))
             return fail(r);
         // default priority (as the context's stream)
-        if ((r = mz_hip(hipStreamCreateWithFlags(&e->s2, hipStreamNonBlocking), "hipStreamCreate")) ||
-            (r = mz_hip(hipEventCreateWithFlags(&e->fork, hipEventDisableTiming), "hipEventCreate")) ||
-            (r = mz_hip(hipEventCreateWithFlags(&e->join, hipEventDisableTiming), "hipEventCreate")))
+        if ((r = mz_hip(hipStreamCreateWithFlags(&e->ls[k], hipStreamNonBlocking), "hipStreamCreate")) ||
+            (r = mz_hip(hipEventCreateWithFlags(&e->join[k], hipEventDisableTiming), "hipEventCreate")))
             return fail(r);
     }
     if ((r = e->alloc(&e->xkvbuf, B * nl * 2 * nh * (size_t)TPAD * HD)) || (r = e->alloc(&e->tok, B * mt)) ||
@@ -456,9 +460,10 @@ static int encode_impl(mz_engine* e, const float* mels, bool on_device, int n, i
     if (!e->loaded) return mz_fail(MZ_ERR_STATE, "mz_engine_encode: weights not loaded (mz_engine_finish)");
     if (n <= 0 || n > e->eg || slot0 < 0 || slot0 + n > e->bmax)
         return mz_fail(MZ_ERR_ARG, "mz_engine_encode: %d clips at slot %d (enc group %d, bmax %d)", n, slot0, e->eg, e->bmax);
-    if (lane && e->trace_on) return mz_fail(MZ_ERR_STATE, "encoder trace on the second lane");
-    hipStream_t s = lane ? e->s2 : e->c->stream;
-    const EncBufs B = lane ? e->lane1 : EncBufs{e->mel, e->melT, e->h1, e->hb, e->qkvh, e->att, e->ff, e->dd, e->ex};
+    if (lane && e->trace_on) return mz_fail(MZ_ERR_STATE, "encoder trace on an extra lane");
+    hipStream_t s = lane ? e->ls[lane - 1] : e->c->stream;
+    const EncBufs B =
+        lane ? e->lanes[lane - 1] : EncBufs{e->mel, e->melT, e->h1, e->hb, e->qkvh, e->att, e->ff, e->dd, e->ex};
     const int D = e->dm.d, nm = e->dm.n_mels, nh = e->dm.nh, F = e->dm.ff, nl = e->dm.dec_layers;
     const int rows = n * TENC;
     const float* src = mels;
@@ -837,16 +842,20 @@ extern "C" int mz_engine_free(mz_engine* e) {
         hipEventDestroy(r.b);
     }
     for (hipEvent_t x : e->evpool) hipEventDestroy(x);
-    if (e->s2) {
-        hipStreamSynchronize(e->s2);
-        hipStreamDestroy(e->s2);
-    }
     if (e->fork) hipEventDestroy(e->fork);
-    if (e->join) hipEventDestroy(e->join);
-    const EncBufs& l = e->lane1;
-    for (void* p : {(void*)l.mel, (void*)l.melT, (void*)l.h1, (void*)l.hb, (void*)l.qkvh, (void*)l.att, (void*)l.ff,
-                    (void*)l.dd, (void*)l.ex, (void*)e->ts_rc, (void*)e->ts_mean, (void*)e->ts_sd, (void*)e->ts_cost,
-                    (void*)e->ts_trace, (void*)e->ts_out})
+    for (int k = 0; k < MZ_ENC_LANES - 1; k++) {
+        if (e->ls[k]) {
+            hipStreamSynchronize(e->ls[k]);
+            hipStreamDestroy(e->ls[k]);
+        }
+        if (e->join[k]) hipEventDestroy(e->join[k]);
+        const EncBufs& l = e->lanes[k];
+        for (void* p : {(void*)l.mel, (void*)l.melT, (void*)l.h1, (void*)l.hb, (void*)l.qkvh, (void*)l.att, (void*)l.ff,
+                        (void*)l.dd, (void*)l.ex})
+            if (p) mz_free(e->c, (uint64_t)(uintptr_t)p);
+    }
+    for (void* p : {(void*)e->ts_rc, (void*)e->ts_mean, (void*)e->ts_sd, (void*)e->ts_cost, (void*)e->ts_trace,
+                    (void*)e->ts_out})
         if (p) mz_free(e->c, (uint64_t)(uintptr_t)p);
     for (void* p : {(void*)e->arena, (void*)e->mel, (void*)e->melT, (void*)e->h1, (void*)e->ex, (void*)e->hb, (void*)e->dd,
                     (void*)e->qkvh, (void*)e->att, (void*)e->ff, (void*)e->trace, (void*)e->xkvbuf, (void*)e->tok,
@@ -877,20 +886,19 @@ static int transcribe_impl(mz_engine* e, const float* mels, bool on_device, cons
     mz_times tm{};
 
     auto t0 = clk::now();
-    // groups alternate between the two encoder lanes (the second waits for the caller's work on the main stream,
-    // the main stream for the second before decoding)
-    const bool two = n > e->eg && !e->trace_on;
-    if (two) {
-        TRY(hipEventRecord(e->fork, e->c->stream), "hipEventRecord");
-        TRY(hipStreamWaitEvent(e->s2, e->fork, 0), "hipStreamWaitEvent");
-    }
+    // groups go round-robin over the encoder lanes (the extra lanes wait for the caller's work on the main stream,
+    // the main stream for them before decoding)
+    const int ngroups = (n + e->eg - 1) / e->eg;
+    const int nlanes = e->trace_on ? 1 : std::min(ngroups, MZ_ENC_LANES);
+    if (nlanes > 1) TRY(hipEventRecord(e->fork, e->c->stream), "hipEventRecord");
+    for (int k = 1; k < nlanes; k++) TRY(hipStreamWaitEvent(e->ls[k - 1], e->fork, 0), "hipStreamWaitEvent");
     for (int g0 = 0, gi = 0; g0 < n; g0 += e->eg, gi++) {
         const int gn = std::min(e->eg, n - g0);
-        if (int r = encode_impl(e, mels + (size_t)g0 * nm * NFR, on_device, gn, g0, two ? gi & 1 : 0)) return r;
+        if (int r = encode_impl(e, mels + (size_t)g0 * nm * NFR, on_device, gn, g0, gi % nlanes)) return r;
     }
-    if (two) {
-        TRY(hipEventRecord(e->join, e->s2), "hipEventRecord");
-        TRY(hipStreamWaitEvent(e->c->stream, e->join, 0), "hipStreamWaitEvent");
+    for (int k = 1; k < nlanes; k++) {
+        TRY(hipEventRecord(e->join[k - 1], e->ls[k - 1]), "hipEventRecord");
+        TRY(hipStreamWaitEvent(e->c->stream, e->join[k - 1], 0), "hipStreamWaitEvent");
     }
     if (int r = mz_sync(e->c)) return r;
     tm.enc = sec(t0);
