@@ -1,5 +1,12 @@
-"""GPU parity of the decoder step at the large-v3-turbo widths (d 1280, 20 heads, 4 layers, ff 5120, vocab 51866) and
-the benchmark's batch of 32 rows, against the oracle's decoder on the same fp16 weights and cross keys/values.
+"""GPU parity at the large-v3-turbo widths (d 1280, 20 heads, ff 5120, 128 mels, vocab 51866).
+
+Encoder: two clips through the conv stem and two layers, every part checked layer-local against the oracle (the
+oracle's layer applied to the engine's own fp32 input of that layer) at max-abs error <= 2e-3 x RMS, as
+test_gpu_engine.py does on the tiny geometry, and the final LayerNorm's fp16 output within one fp16 ulp: this covers
+the products and the attention at the full widths with the clip and head indexing of a group of more than one clip.
+
+Decoder: the benchmark's batch of 32 rows through 4 layers, against the oracle's decoder on the same fp16 weights and
+cross keys/values.
 
 The tiny geometry of test_gpu_engine.py runs every decoder kernel, but only at its own sizes: this file covers the
 configurations the benchmark runs and the tiny model never reaches — split-K slices of 256 and 1024, the QKV and fc1
@@ -28,6 +35,38 @@ def rel_err(got, ref):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     return np.abs(got - ref).max() / np.sqrt((ref ** 2).mean())
+
+
+def test_encoder_turbo_widths_layer_local():
+    g = synth.Geometry(d=1280, ff=5120, nh=20, enc_layers=2, dec_layers=1, n_mels=128, vocab=51866)
+    W = synth.random_weights(g, seed=6, bias_std=0.02, ln_std=0.1)
+    Wf = {k: v.astype(np.float32) for k, v in W.items() if k.startswith("model.encoder")}
+    gen = synth.generation_config(g, align_heads=[[0, 0]])
+    dims = model.Dims(g.d, g.ff, g.nh, g.enc_layers, g.dec_layers, g.n_mels, g.vocab, g.max_t)
+    ctx = model.Context(0)
+    e = model.Engine(ctx, dims, model.GenCfg.from_dict(gen, dims), 2, 2)
+    e.load(W)
+    mel = synth.synthetic_mel(2, g.n_mels, seed=9)
+    e.set_trace(True)
+    e.encode(mel, 0)
+    tr = e.trace(2)  # [L][n][1500][d] inputs of every layer
+    xl = e.read(L.BUF_ENC_X, np.float32, (2, 1500, g.d))
+    out = e.enc_out(2).astype(np.float32)
+    for c in range(2):
+        m16 = mel[c].astype(np.float16).astype(np.float32)
+        errs = [rel_err(tr[0, c], R.conv_stem(m16, Wf))]
+        for i in range(g.enc_layers):
+            nxt = tr[i + 1, c] if i + 1 < g.enc_layers else xl[c]
+            errs.append(rel_err(nxt, R.encoder_layer(tr[i, c], Wf, i, g.nh)))
+        # the final LayerNorm's fp16 output: within one fp16 ulp of the oracle's value (its max-abs error alone is
+        # ~2e-3 x RMS from the rounding of the largest outputs)
+        ref = R.layer_norm(xl[c], Wf["model.encoder.layer_norm.weight"], Wf["model.encoder.layer_norm.bias"])
+        ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float32)
+        assert np.all(np.abs(out[c] - ref) <= ulp), np.abs(out[c] - ref).max()
+        print("turbo widths, clip", c, ["%.2e" % x for x in errs])
+        assert max(errs) < 2e-3, errs
+    e.close()
+    ctx.close()
 
 
 def test_decoder_turbo_widths_batch32():
