@@ -52,7 +52,8 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
     const int nbn = (p.N + BN - 1) / BN, nbm = (p.M + BM - 1) / BM;
     int bm, bn;
     if (!xcd_tile(blockIdx.x, nbm, nbn, &bm, &bn)) return;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index through readfirstlane: wave-uniform values (tile origins, store descriptors) stay scalar
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 2, wn = wave & 3, lr = lane & 31, lh = lane >> 5;
     const int nk = p.K >> 6;
     // this lane's slot in a direct load: row lrow of an 8-row slice, 16-byte chunk lc of the row
@@ -186,6 +187,71 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
             return;
         }
     }
+    // row offsets of accumulator element r within a 32-row product: 8 (r / 4) + r % 4 (+ 4 for the upper half-wave)
+    if (EPI == EPI_HEADS) {
+        // q and k tiles (and every tile of kind 2) are row-major [t][64]. M is a whole number of clips, and a
+        // wave's 128 rows span at most two of them (128 < 1500): the store descriptor starts at the first one's
+        // tiles and ends after the second one, or after the last clip of the call, so the range check drops the
+        // rows of a partial last tile. Rows of the second clip add one clip's worth of tiles; every offset stays
+        // below 2^31 bytes (two clips of at most 1024 tiles).
+        const int g0 = m0 / MZ_TENC;
+        const long clip = (long)p.blocks_per_clip * (MZ_TPAD * MZ_HD);
+        const int ncl = min(p.M / MZ_TENC - g0, 2);
+        const __amdgpu_buffer_rsrc_t rH =
+            rsrc(p.heads + (p.slot0 + g0) * clip, ncl > 0 ? (unsigned)(ncl * clip * 2) : 0u);
+        const int blk = n0 >> 6, c0 = (n0 & 63) + lr;
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int mb = m0 + i * 32 + 4 * lh, gb = mb / MZ_TENC, tb = mb - gb * MZ_TENC;
+            const unsigned cb = (unsigned)((gb - g0) * clip + (long)blk * (MZ_TPAD * MZ_HD)) + c0 + tb * MZ_HD;
+            // frame tb + dr >= 1500 is frame tb + dr - 1500 of the next clip
+            const unsigned wrap = (unsigned)(clip - MZ_TENC * MZ_HD);
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int n = n0 + j * 32 + lr;
+                const float bv = p.bias ? (float)p.bias[min(n, p.N - 1)] : 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int dr = 8 * (r >> 2) + (r & 3);
+                    const unsigned e = cb + j * 32 + dr * MZ_HD + (tb + dr >= MZ_TENC ? wrap : 0u);
+                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (f16)(acc[i][j][r] + bv)), rH,
+                                                          e * 2, 0, 0);
+                }
+            }
+        }
+        return;
+    }
+    if (EPI == EPI_F16 || EPI == EPI_GELU_F16 || EPI == EPI_RESID_F32) {
+        // buffer stores over exactly M rows: the range check drops the rows of a partial last tile, and every
+        // offset is one lane base plus a wave-uniform row offset
+        constexpr unsigned ES = EPI == EPI_RESID_F32 ? 4 : 2;
+        const __amdgpu_buffer_rsrc_t rO = rsrc(p.out, (unsigned)(p.M * p.ldo) * ES);
+        const unsigned rs = (unsigned)p.ldo * ES;
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + j * 32 + lr;
+            if (n >= p.N) continue;
+            const float bv = p.bias ? (float)p.bias[n] : 0.f;
+            const unsigned vb = (unsigned)((m0 + 4 * lh) * p.ldo + n) * ES;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const unsigned off = vb + (unsigned)(i * 32 + 8 * (r >> 2) + (r & 3)) * rs;
+                    const float v = acc[i][j][r] + bv;
+                    if (EPI == EPI_F16) {
+                        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (f16)v), rO, off, 0, 0);
+                    } else if (EPI == EPI_GELU_F16) {
+                        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (f16)gelu_erf(v)), rO, off, 0, 0);
+                    } else {
+                        const float o = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rO, off, 0, 0));
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, o + v), rO, off, 0, 0);
+                    }
+                }
+        }
+        return;
+    }
+    // EPI_GELU_POS (the conv stem's second product, once per encoder pass)
 #pragma unroll
     for (int j = 0; j < TN; j++) {
         const int n = n0 + j * 32 + lr;
@@ -198,20 +264,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
                 const int m = m0 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                 if (m >= p.M) continue;
                 const float v = acc[i][j][r] + bv;
-                if (EPI == EPI_F16) {
-                    ((f16*)p.out)[(long)m * p.ldo + n] = (f16)v;
-                } else if (EPI == EPI_GELU_F16) {
-                    ((f16*)p.out)[(long)m * p.ldo + n] = (f16)gelu_erf(v);
-                } else if (EPI == EPI_RESID_F32) {
-                    float* o = (float*)p.out + (long)m * p.ldo + n;
-                    *o += v;
-                } else if (EPI == EPI_GELU_POS) {
-                    ((float*)p.out)[(long)m * p.ldo + n] = gelu_erf(v) + (float)p.pos[(long)(m % MZ_TENC) * p.N + n];
-                } else if (EPI == EPI_HEADS) {
-                    const int g = m / MZ_TENC, t = m - g * MZ_TENC;
-                    p.heads[((long)(p.slot0 + g) * p.blocks_per_clip + (n >> 6)) * (MZ_TPAD * MZ_HD) +
-                            (long)t * MZ_HD + (n & 63)] = (f16)v;
-                }
+                ((float*)p.out)[(long)m * p.ldo + n] = gelu_erf(v) + (float)p.pos[(long)(m % MZ_TENC) * p.N + n];
             }
     }
 #endif
@@ -239,7 +292,12 @@ hipError_t pick(hipStream_t s, const MzGemm& g) {
 
 hipError_t mz_gemm_launch(hipStream_t s, int aload, int epi, const MzGemm& g) {
     if (g.K % 64 != 0 || g.M <= 0 || g.N <= 0 || g.K <= 0 || g.N % 4 != 0) return hipErrorInvalidValue;
-    if (epi == EPI_HEADS && g.N % 64 != 0) return hipErrorInvalidValue;
+    if (epi == EPI_HEADS && (g.N % 64 != 0 || g.M % MZ_TENC != 0 || g.blocks_per_clip <= 0 || g.blocks_per_clip > 1024))
+        return hipErrorInvalidValue;
+    // the store descriptors address the output with 32-bit byte offsets
+    if ((epi == EPI_F16 || epi == EPI_GELU_F16 || epi == EPI_RESID_F32) &&
+        (long)g.M * g.ldo * (epi == EPI_RESID_F32 ? 4 : 2) >= (1L << 31))
+        return hipErrorInvalidValue;
     if (aload == ALOAD_CONV) {
         if (g.conv_cin % 8 != 0 || g.conv_tout <= 0) return hipErrorInvalidValue;
         if (epi == EPI_GELU_F16) return pick<ALOAD_CONV, EPI_GELU_F16>(s, g);

@@ -189,13 +189,14 @@ def test_gemm_head_scatter(ctx, kind):
     x, w, b = f16(rng, (m, k)), f16(rng, (n, k), 0.1), f16(rng, (n,), 0.1)
     dx, dw, db = (ctx.upload_new(a) for a in (x, w, b))
     bpc = groups * nh
-    nslots = slot0 + clips
+    nslots = slot0 + clips + 1  # one slot past the call's clips, which must stay untouched
     dh = ctx.alloc(nslots * bpc * TPAD * 64 * 2)
     L.check(L.lib().mz_linear(ctx.h, linear_args(epilogue=L.EPI_HEADS, a=dx, lda=k, w=dw, bias=db, m=m, n=n, k=k,
                                                  heads=dh, blocks_per_clip=bpc, nh=nh, kind=kind, slot0=slot0)))
     got = ctx.download(dh, (nslots, bpc, TPAD * 64), np.float16)
     ref = (x.astype(np.float64) @ w.astype(np.float64).T + b).reshape(clips, 1500, bpc, 64)
     assert not got[:slot0].any(), "a slot before slot0 was written"
+    assert not got[slot0 + clips:].any(), "a slot after the last clip was written"
     for c in range(clips):
         for blk in range(bpc):
             tile = got[slot0 + c, blk]
