@@ -26,28 +26,30 @@
 namespace {
 
 
-// sum over a workgroup whose size is a multiple of 64 (at most 1024); red holds 16 floats
-__device__ __forceinline__ float block_sum(float v, float* red) {
-    v = wave_sum(v);
-    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+// LayerNorm of one row held as v = x[4t .. 4t + 3] by thread t (threads with 4t >= dim hold zeros), written as fp16;
+// gamma / beta come in already loaded. Each wave takes the mean and the sum of squared deviations of its own
+// elements (two passes over registers), and one exchange through LDS combines the waves' pairs (Chan et al.'s
+// pairwise update): one barrier per row. The workgroup is at most 16 waves; red holds 16 pairs.
+__device__ __forceinline__ void ln_row4(float4 v, bool on, int dim, f16x4 wv, f16x4 bv, f16* __restrict__ y,
+                                       float eps, float2* red) {
+    const int c = 4 * threadIdx.x, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const float nk = (float)min(256, dim - 256 * wave);  // elements of this wave (every wave holds at least 4)
+    const float mk = wave_sum(on ? v.x + v.y + v.z + v.w : 0.f) / nk;
+    const float ex = v.x - mk, ey = v.y - mk, ez = v.z - mk, ew = v.w - mk;
+    const float qk = wave_sum(on ? ex * ex + ey * ey + ez * ez + ew * ew : 0.f);
+    if ((threadIdx.x & 63) == 0) red[wave] = make_float2(mk, qk);
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    float s = 0.f;
-    for (int i = 0; i < nw; i++) s += red[i];
-    return s;
-}
-
-// LayerNorm of one row held as v = x[4t .. 4t + 3] by thread t (threads with 4t >= dim hold zeros), written as fp16
-__device__ __forceinline__ void ln_row4(float4 v, bool on, int dim, const f16* __restrict__ w,
-                                        const f16* __restrict__ b, f16* __restrict__ y, float eps, float* red) {
-    const int c = 4 * threadIdx.x;
-    const float mean = block_sum(on ? v.x + v.y + v.z + v.w : 0.f, red) / dim;
-    const float dx = v.x - mean, dy = v.y - mean, dz = v.z - mean, dw = v.w - mean;
-    const float var = block_sum(on ? dx * dx + dy * dy + dz * dz + dw * dw : 0.f, red) / dim;
-    const float rstd = rsqrtf(var + eps);
+    float mean = 0.f;
+    for (int i = 0; i < nw; i++) mean += (float)min(256, dim - 256 * i) * red[i].x;
+    mean /= dim;
+    float m2 = 0.f;
+    for (int i = 0; i < nw; i++) {
+        const float d = red[i].x - mean;
+        m2 += red[i].y + (float)min(256, dim - 256 * i) * d * d;
+    }
+    const float rstd = rsqrtf(m2 / dim + eps);
     if (on) {
-        const f16x4 wv = *(const f16x4*)(w + c), bv = *(const f16x4*)(b + c);
+        const float dx = v.x - mean, dy = v.y - mean, dz = v.z - mean, dw = v.w - mean;
         st4(y + c, dx * rstd * (float)wv[0] + (float)bv[0], dy * rstd * (float)wv[1] + (float)bv[1],
             dz * rstd * (float)wv[2] + (float)bv[2], dw * rstd * (float)wv[3] + (float)bv[3]);
     }
@@ -59,17 +61,22 @@ __global__ void __launch_bounds__(512) dec_add_ln_kernel(float* __restrict__ x, 
                                                          int nparts, long part_stride, const f16* __restrict__ bias,
                                                          const f16* __restrict__ w, const f16* __restrict__ b,
                                                          f16* __restrict__ y, int dim, float eps) {
-    __shared__ float red[16];
+    __shared__ float2 red[16];
     const int row = blockIdx.x, c = 4 * threadIdx.x;
     const bool on = c < dim;
     float4 v = {0.f, 0.f, 0.f, 0.f};
+    f16x4 wv = {}, bv = {};
     if (on) {
+        // every load of the row is issued before the first use
         const long idx = (long)row * dim + c;
         float4 pp[MZ_MAX_PARTS];
 #pragma unroll
         for (int s = 0; s < MZ_MAX_PARTS; s++)
             if (s < nparts) pp[s] = *(const float4*)(parts + s * part_stride + idx);
         v = *(const float4*)(x + idx);
+        const f16x4 bb = bias ? *(const f16x4*)(bias + c) : f16x4{};
+        wv = *(const f16x4*)(w + c);
+        bv = *(const f16x4*)(b + c);
 #pragma unroll
         for (int s = 0; s < MZ_MAX_PARTS; s++)
             if (s < nparts) {
@@ -78,16 +85,13 @@ __global__ void __launch_bounds__(512) dec_add_ln_kernel(float* __restrict__ x, 
                 v.z += pp[s].z;
                 v.w += pp[s].w;
             }
-        if (bias) {
-            const f16x4 bb = *(const f16x4*)(bias + c);
-            v.x += (float)bb[0];
-            v.y += (float)bb[1];
-            v.z += (float)bb[2];
-            v.w += (float)bb[3];
-        }
+        v.x += (float)bb[0];
+        v.y += (float)bb[1];
+        v.z += (float)bb[2];
+        v.w += (float)bb[3];
         *(float4*)(x + idx) = v;
     }
-    ln_row4(v, on, dim, w, b, y + (long)row * dim, eps, red);
+    ln_row4(v, on, dim, wv, bv, y + (long)row * dim, eps, red);
 }
 
 __global__ void __launch_bounds__(512) dec_embed_ln_kernel(const int* __restrict__ tok, int* __restrict__ ctr,
@@ -95,11 +99,16 @@ __global__ void __launch_bounds__(512) dec_embed_ln_kernel(const int* __restrict
                                                            float* __restrict__ x, const f16* __restrict__ w,
                                                            const f16* __restrict__ b, f16* __restrict__ y, int dim,
                                                            int maxT, float eps) {
-    __shared__ float red[16];
+    __shared__ float2 red[16];
     const int row = blockIdx.x, c = 4 * threadIdx.x;
+    const bool on = c < dim;
+    f16x4 wv = {}, bv = {};
+    if (on) {
+        wv = *(const f16x4*)(w + c);
+        bv = *(const f16x4*)(b + c);
+    }
     const int p = min(ctr[0], maxT - 1);
     if (row == 0 && threadIdx.x == 0) ctr[1] = p;  // the position of this step, for its later kernels
-    const bool on = c < dim;
     float4 v = {0.f, 0.f, 0.f, 0.f};
     if (on) {
         const int t = tok[(long)row * maxT + p];
@@ -107,7 +116,7 @@ __global__ void __launch_bounds__(512) dec_embed_ln_kernel(const int* __restrict
         v = {(float)e[0] + (float)q[0], (float)e[1] + (float)q[1], (float)e[2] + (float)q[2], (float)e[3] + (float)q[3]};
         *(float4*)(x + (long)row * dim + c) = v;
     }
-    ln_row4(v, on, dim, w, b, y + (long)row * dim, eps, red);
+    ln_row4(v, on, dim, wv, bv, y + (long)row * dim, eps, red);
 }
 
 // ---------------------------------------------------------------- skinny GEMM
