@@ -146,6 +146,12 @@ int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, int bmax, int
 int mz_engine_put(mz_engine* e, const char* name, int dtype, const void* data, const int64_t* shape, int ndim);
 /* Checks every tensor was placed (Arena::finish, src/gpu.rs:363-373). */
 int mz_engine_finish(mz_engine* e);
+/* Every tensor of <model_dir>/model.safetensors through mz_engine_put, then mz_engine_finish (the Loader over the
+ * mapped checkpoint, src/model.rs:200-265 with src/st.rs; F16 and F32 tensors, anything else is an error). */
+int mz_engine_load(mz_engine* e, const char* model_dir);
+/* Engine::new (src/model.rs:333-514) from a Hugging Face model directory: config.json and generation_config.json
+ * through mz_model_open, mz_engine_new, then mz_engine_load. */
+int mz_engine_open(mz_ctx* c, const char* model_dir, int bmax, int eg, mz_engine** out);
 /* Encoder for n <= eg clips of log-mel f32 [n][n_mels][3000] (host); writes every decoder layer's cross k/v into
  * decoder slots slot0 .. slot0 + n - 1 (Engine::encode, src/model.rs:545-625). */
 int mz_engine_encode(mz_engine* e, const float* mels, int n, int slot0);
@@ -226,6 +232,40 @@ int mz_transcribe_device(mz_engine* e, uint64_t mels, const int32_t* frames, int
  * Odd width <= 15. Allocates and frees its own device scratch; synchronous on the context's stream. */
 int mz_jump_times_device(mz_ctx* c, uint64_t w, int64_t clip_stride, int n, const int32_t* rows, const int32_t* cols,
                          int heads, int cols_full, int width, int half, float* out, int64_t out_stride);
+
+/* ------------------------------------------------------------------ model directory (host only) */
+
+/* Safetensors file (st::File, src/st.rs:77-181): mapped read-only (read into memory if mapping fails), header
+ * checked as st.rs:93-142 does (header length, an object header, known dtypes, integer shapes, two data offsets
+ * in order and inside the data, size = elements x element size, no duplicate names, no overlapping ranges).
+ * Tensors keep the header's order; data pointers stay valid until mz_st_close. */
+typedef struct mz_st mz_st;
+int mz_st_open(const char* path, mz_st** out);
+int mz_st_count(const mz_st* f, int* n);
+/* Tensor i: name, dtype ("F16", "F32", ...), rank, shape, data and byte count (any output may be null). */
+int mz_st_info(const mz_st* f, int i, const char** name, const char** dtype, int* ndim, const int64_t** shape,
+               const void** data, uint64_t* bytes);
+/* Index of a tensor by name (File::get's lookup, st.rs:144-147); MZ_ERR_ARG "missing tensor" if absent. */
+int mz_st_find(const mz_st* f, const char* name, int* i);
+/* A __metadata__ string entry (File::meta). */
+int mz_st_meta(const mz_st* f, const char* key, const char** value);
+int mz_st_close(mz_st* f);
+/* MZ_OK if s[0 .. n) is one JSON value under the strict grammar of src/json.rs:1-218, else MZ_ERR_ARG with the
+ * parser's message (the same parser reads the safetensors header and the configs). */
+int mz_json_check(const char* s, size_t n);
+
+/* A model directory's configs: Dims::load (src/model.rs:33-61) on config.json and GenCfg::load (:78-146) on
+ * generation_config.json, with the same range checks and defaults (alignment heads: every head of the second half
+ * of the decoder layers). The arrays mz_model_gencfg points to live until mz_model_free. */
+typedef struct mz_model mz_model;
+int mz_model_open(const char* model_dir, mz_model** out);
+int mz_model_dims(const mz_model* m, mz_dims* d);
+int mz_model_gencfg(const mz_model* m, mz_gencfg* g);
+/* Language i (code with "<|" "|>" stripped, token) of lang_to_id, and task i (name, token) of task_to_id, in file
+ * order (GenCfg::langs / tasks). */
+int mz_model_lang(const mz_model* m, int i, const char** code, int32_t* token);
+int mz_model_task(const mz_model* m, int i, const char** name, int32_t* token);
+int mz_model_free(mz_model* m);
 
 /* ------------------------------------------------------------------ host helpers */
 

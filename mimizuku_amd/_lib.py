@@ -78,6 +78,22 @@ SIGNATURES = {
     "mz_engine_new": (i32, [P, C.POINTER(Dims), C.POINTER(GenCfgC), i32, i32, C.POINTER(P)]),
     "mz_engine_put": (i32, [P, C.c_char_p, i32, P, C.POINTER(C.c_int64), i32]),
     "mz_engine_finish": (i32, [P]),
+    "mz_engine_load": (i32, [P, C.c_char_p]),
+    "mz_engine_open": (i32, [P, C.c_char_p, i32, i32, C.POINTER(P)]),
+    "mz_st_open": (i32, [C.c_char_p, C.POINTER(P)]),
+    "mz_st_count": (i32, [P, C.POINTER(i32)]),
+    "mz_st_info": (i32, [P, i32, C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), C.POINTER(i32),
+                         C.POINTER(C.POINTER(C.c_int64)), C.POINTER(P), C.POINTER(u64)]),
+    "mz_st_find": (i32, [P, C.c_char_p, C.POINTER(i32)]),
+    "mz_st_meta": (i32, [P, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "mz_st_close": (i32, [P]),
+    "mz_json_check": (i32, [C.c_char_p, sz]),
+    "mz_model_open": (i32, [C.c_char_p, C.POINTER(P)]),
+    "mz_model_dims": (i32, [P, C.POINTER(Dims)]),
+    "mz_model_gencfg": (i32, [P, C.POINTER(GenCfgC)]),
+    "mz_model_lang": (i32, [P, i32, C.POINTER(C.c_char_p), C.POINTER(C.c_int32)]),
+    "mz_model_task": (i32, [P, i32, C.POINTER(C.c_char_p), C.POINTER(C.c_int32)]),
+    "mz_model_free": (i32, [P]),
     "mz_engine_encode": (i32, [P, P, i32, i32]),
     "mz_engine_encode_device": (i32, [P, u64, i32, i32]),
     "mz_engine_profile": (i32, [P, i32]),

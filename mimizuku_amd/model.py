@@ -9,8 +9,6 @@ from __future__ import annotations
 
 import ctypes as C
 import dataclasses
-import json
-import os
 import weakref
 
 import numpy as np
@@ -103,22 +101,8 @@ class Dims:
 
     @staticmethod
     def load(model_dir: str) -> "Dims":
-        with open(os.path.join(model_dir, "config.json")) as f:
-            c = json.load(f)
-
-        def n(k):
-            v = c.get(k)
-            if not isinstance(v, int) or isinstance(v, bool) or not (1 <= v < 1 << 20):
-                raise MzError(f"config.json: {k} missing or out of range")
-            return v
-
-        d = Dims(n("d_model"), n("encoder_ffn_dim"), n("encoder_attention_heads"), n("encoder_layers"),
-                 n("decoder_layers"), n("num_mel_bins"), n("vocab_size"), n("max_target_positions"))
-        if d.nh * 64 != d.d or n("decoder_attention_heads") != d.nh or n("decoder_ffn_dim") != d.ff:
-            raise MzError(f"unsupported shape {d}: the kernels need 64-wide heads and equal encoder/decoder widths")
-        if n("max_source_positions") != TENC:
-            raise MzError(f"unsupported shape {d}: max_source_positions must be {TENC}")
-        return d
+        """config.json through the library's own reader (mz_model_open: strict JSON, the same range checks)."""
+        return ModelDir(model_dir).dims
 
     def c(self) -> L.Dims:
         return L.Dims(*dataclasses.astuple(self))
@@ -165,9 +149,9 @@ class GenCfg:
                       [tok(t) for t in (g.get("suppress_tokens") or [])], bs, heads)
 
     @staticmethod
-    def load(model_dir: str, dims: Dims) -> "GenCfg":
-        with open(os.path.join(model_dir, "generation_config.json")) as f:
-            return GenCfg.from_dict(json.load(f), dims)
+    def load(model_dir: str, dims: Dims | None = None) -> "GenCfg":
+        """generation_config.json through the library's own reader (mz_model_open)."""
+        return ModelDir(model_dir).gencfg
 
     def lang_token(self, code: str):
         return next((t for c, t in self.langs if c == code), None)
@@ -183,6 +167,45 @@ class GenCfg:
         s = L.GenCfgC(self.sot, self.eos, self.no_timestamps, p[0], len(self.suppress), p[1], len(self.begin_suppress),
                       p[2], len(self.langs), p[3], len(self.align_heads))
         return s, arrs
+
+
+class ModelDir:
+    """A Hugging Face model directory read by the library (mz_model_open: config.json -> Dims, src/model.rs:33-61;
+    generation_config.json -> GenCfg, :78-146). from_dict above is the same reading of an in-memory dict."""
+
+    def __init__(self, model_dir: str):
+        h = C.c_void_p()
+        check(L.lib().mz_model_open(model_dir.encode(), C.byref(h)))
+        try:
+            lib = L.lib()
+            dc = L.Dims()
+            check(lib.mz_model_dims(h, C.byref(dc)))
+            self.dims = Dims(*[getattr(dc, f.name) for f in dataclasses.fields(Dims)])
+            g = L.GenCfgC()
+            check(lib.mz_model_gencfg(h, C.byref(g)))
+            arr = lambda p, n: [int(p[i]) for i in range(n)]  # noqa: E731
+            heads = arr(g.align_heads, 2 * g.n_align)
+
+            def entries(fn, n):
+                out = []
+                for i in range(n):
+                    name, tok = C.c_char_p(), C.c_int32()
+                    check(fn(h, i, C.byref(name), C.byref(tok)))
+                    out.append((name.value.decode(), tok.value))
+                return out
+            langs = entries(lib.mz_model_lang, g.n_langs)
+            tasks, i = [], 0
+            while True:  # task_to_id entries (the count is not part of mz_gencfg)
+                name, tok = C.c_char_p(), C.c_int32()
+                if lib.mz_model_task(h, i, C.byref(name), C.byref(tok)) != 0:
+                    break
+                tasks.append((name.value.decode(), tok.value))
+                i += 1
+            self.gencfg = GenCfg(g.sot, g.eos, g.no_timestamps, langs, tasks, arr(g.suppress, g.n_suppress),
+                                 arr(g.begin_suppress, g.n_begin_suppress),
+                                 [(heads[2 * k], heads[2 * k + 1]) for k in range(g.n_align)])
+        finally:
+            L.lib().mz_model_free(h)
 
 
 def scratch_bytes(dims: Dims, na: int, bmax: int, eg: int) -> int:
@@ -206,12 +229,11 @@ class Engine:
 
     @staticmethod
     def new(model_dir: str, bmax: int, eg: int, ctx: Context | None = None) -> "Engine":
-        """Engine for a Hugging Face model directory (config.json, generation_config.json, model.safetensors)."""
-        from safetensors.numpy import load_file
-        dims = Dims.load(model_dir)
-        gc = GenCfg.load(model_dir, dims)
-        e = Engine(ctx or Context(), dims, gc, bmax, eg)
-        e.load(load_file(os.path.join(model_dir, "model.safetensors")))
+        """Engine for a Hugging Face model directory (config.json, generation_config.json, model.safetensors), read
+        by the library: the configs through mz_model_open, the mapped checkpoint through mz_engine_load."""
+        md = ModelDir(model_dir)
+        e = Engine(ctx or Context(), md.dims, md.gencfg, bmax, eg)
+        check(L.lib().mz_engine_load(e.h, model_dir.encode()))
         return e
 
     def load(self, weights: dict):

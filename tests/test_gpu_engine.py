@@ -162,6 +162,25 @@ def test_graph_replay_equals_eager(ctx, case):
     np.testing.assert_array_equal(x1, x2)
 
 
+def test_engine_from_model_dir_equals_put(ctx, case, tmp_path):
+    """Engine.new reads the directory in the library (configs, mapped safetensors, F32 -> F16 on the host) and
+    places the same bits as tensors handed over one by one: identical tokens, logits and alignment rows."""
+    W32 = {k: v.astype(np.float32) for k, v in case.W.items()}  # the checkpoint in F32, converted by the library
+    synth.write_model_dir(str(tmp_path), G, W32, case.gen)
+    res = []
+    for from_dir in (True, False):
+        e = model.Engine.new(str(tmp_path), case.n, case.n, ctx=ctx) if from_dir else case.engine(ctx)
+        assert e.dims == case.dims and e.gc == case.gc
+        p = transcribe.Prompt(e.gc, "auto" if case.detect else "en")
+        out, _ = transcribe.transcribe(e, case.mel, p, max_new=12)
+        res.append(([d.seq for d in out], [d.ts for d in out], e.logits(), e.align()))
+        e.close()
+    (s1, t1, l1, a1), (s2, t2, l2, a2) = res
+    assert s1 == s2 and t1 == t2
+    np.testing.assert_array_equal(l1, l2)
+    np.testing.assert_array_equal(a1, a2)
+
+
 def test_step_beyond_the_cache_is_refused(ctx):
     case_dims = model.Dims(G.d, G.ff, G.nh, 1, 1, G.n_mels, G.vocab, 16)
     gen = synth.generation_config(G, align_heads=[[0, 0]])
