@@ -267,6 +267,24 @@ int mz_model_lang(const mz_model* m, int i, const char** code, int32_t* token);
 int mz_model_task(const mz_model* m, int i, const char** name, int32_t* token);
 int mz_model_free(mz_model* m);
 
+/* ------------------------------------------------------------------ audio front end (src/audio.rs) */
+
+/* read_wav (src/audio.rs:14-75): mono samples of a RIFF/WAVE file (16/24/32-bit PCM or 32-bit float, channels
+ * averaged; a data size of 0xFFFFFFFF runs to the end of the file) and its sample rate. *n and *sr are always set;
+ * the samples are written only when y is non-null and cap >= *n (call once with y = NULL to size the buffer). */
+int mz_wav_read(const char* path, float* y, size_t cap, size_t* n, int* sr);
+/* to_16k (src/audio.rs:77-145): Kaiser-windowed sinc resampling to 16 kHz in double, rates 1 kHz .. 768 kHz;
+ * *n_out always set, out written when non-null and cap >= *n_out. */
+int mz_resample_16k(const float* y, size_t n, int sr, float* out, size_t cap, size_t* n_out);
+/* Mel::new's tables (src/audio.rs:161-189): Slaney filters f32 [201][n_mels] up to 8 kHz, and the
+ * periodic-Hann-windowed DFT basis cos / sin f64 [400][201] (sample-major); any output may be null. */
+int mz_mel_tables(int n_mels, float* filters, double* cosb, double* sinb);
+/* Mel::features (src/audio.rs:195-249) of n clips on the device: audio f32 [n][480000] at device address `audio`
+ * (16 kHz; samples at or past n_samples[i] read as zero) -> normalised log-mel f32 [n][n_mels][3000] at `mel`;
+ * frames[i] (may be null) = 10 ms frames that hold audio. The power spectra equal the reference's bit for bit
+ * (double sums in sample order); log10 is the device library's. Synchronous; allocates and frees its scratch. */
+int mz_log_mel(mz_ctx* c, uint64_t audio, const int32_t* n_samples, int n, int n_mels, uint64_t mel, int32_t* frames);
+
 /* ------------------------------------------------------------------ host helpers */
 
 /* Token start times from alignment-head weights w [rows][heads][cols_full] (f32), cropped to cols frames

@@ -147,3 +147,25 @@ struct MzTs {
 // scratch elements per clip for cost / trace
 inline long mz_ts_diag_stride(int rmax, int cols_full) { return (long)(rmax + cols_full + 1) * (rmax + 1); }
 hipError_t mz_ts_launch(hipStream_t s, const MzTs& p, int n);
+
+// ---------------------------------------------------------------- log-mel features (Mel::features, src/audio.rs)
+#define MZ_MEL_NFFT 400
+#define MZ_MEL_HOP 160
+#define MZ_MEL_BINS 201          // MZ_MEL_NFFT / 2 + 1
+#define MZ_MEL_NSAMPLES 480000   // 30 s at 16 kHz
+#define MZ_NFR_HOST 3000         // log-mel frames of 30 s
+// audio [n][480000] f32 (samples at or past ns[c] read as zero), tables from mz_mel_tables (cosb / sinb
+// [400][201] windowed DFT basis, filt [201][n_mels]); pow [n][3000][201] and mx [n] are scratch;
+// mel [n][n_mels][3000] the normalised log-mel
+struct MzMel {
+    const float* audio;
+    const int* ns;
+    const double* cosb;
+    const double* sinb;
+    const float* filt;
+    float* pow;
+    float* mx;
+    float* mel;
+    int n, n_mels;
+};
+hipError_t mz_log_mel_launch(hipStream_t s, const MzMel& p);
