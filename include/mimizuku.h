@@ -285,6 +285,40 @@ int mz_mel_tables(int n_mels, float* filters, double* cosb, double* sinb);
  * (double sums in sample order); log10 is the device library's. Synchronous; allocates and frees its scratch. */
 int mz_log_mel(mz_ctx* c, uint64_t audio, const int32_t* n_samples, int n, int n_mels, uint64_t mel, int32_t* frames);
 
+/* ------------------------------------------------------------------ text (src/tok.rs, src/main.rs) */
+
+/* Decoding side of the byte-level BPE tokenizer (Tok, src/tok.rs): <model_dir>/vocab.json through the GPT-2
+ * byte table; ids must be below vocab and every id below eos needs an entry (Tok::load, :25-45). */
+typedef struct mz_tok mz_tok;
+int mz_tok_open(const char* model_dir, int vocab, int eos, mz_tok** out);
+/* A tokenizer over raw byte strings entries[i] of lens[i] bytes (id i), for callers with their own vocabulary. */
+int mz_tok_from_bytes(const char* const* entries, const size_t* lens, int n, mz_tok** out);
+int mz_tok_free(mz_tok* t);
+/* Tok::decode (:47-57): the ids' bytes (unknown ids dropped) as UTF-8 with invalid sequences replaced by U+FFFD,
+ * then the clean-up of spaces before punctuation and contractions. Text out NUL-terminated when cap > *len. */
+int mz_tok_decode(const mz_tok* t, const int32_t* ids, int n, char* out, size_t cap, size_t* len);
+/* Tok::pieces (:63-86): whole UTF-8 pieces of the tokens below eos with start / end times; the pieces' text is
+ * concatenated into text (NUL-terminated when cap > *len), piece k spanning offsets[k] .. offsets[k + 1]
+ * (offsets holds n + 1 entries, t0 / t1 n), *n_pieces set; any of text / offsets / t0 / t1 may be null. */
+int mz_tok_pieces(const mz_tok* t, const int32_t* ids, const float* ts, int n, int eos, char* text, size_t cap,
+                  size_t* len, int32_t* offsets, float* t0, float* t1, int* n_pieces);
+/* A time as the CLI's JSON prints it: Python's round(x, 2) as json.dumps writes a float (json_t, main.rs:113-117). */
+int mz_json_time(float x, char* out, size_t cap, size_t* len);
+/* to_json (src/main.rs:121-138): {path: {"language", "text", "words": [[piece, start, end], ...]}, ...} plus a
+ * newline for n clips; clip i's tokens seq[i * stride ..] (seq_len[i] of them, prompt included), times ts likewise,
+ * detected language token langs[i] ("en" for an English-only model). Out NUL-terminated when cap > *len. */
+int mz_results_json(const mz_tok* t, const mz_model* m, int n, const char* const* paths, const int32_t* seq,
+                    const int32_t* seq_len, int stride, const float* ts, const int32_t* langs, char* out, size_t cap,
+                    size_t* len);
+
+/* ------------------------------------------------------------------ command line (src/main.rs) */
+
+/* The mimizuku command line (main.rs:17-224): argv[0] is the program name; --model DIR, input WAV files or --dir /
+ * --prefix, --language, --task, --out, --batch, --enc-group, --quiet, --no-graph, --help. Prints the JSON to
+ * stdout (or --out) and the reference's progress and timing lines to stderr; returns the process exit status
+ * (errors print "error: ..." and return 1). Uses device 0 with its own context. */
+int mz_cli(int argc, const char* const* argv);
+
 /* ------------------------------------------------------------------ host helpers */
 
 /* Token start times from alignment-head weights w [rows][heads][cols_full] (f32), cropped to cols frames

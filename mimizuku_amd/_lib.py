@@ -113,6 +113,14 @@ SIGNATURES = {
     "mz_resample_16k": (i32, [P, sz, i32, P, sz, C.POINTER(sz)]),
     "mz_mel_tables": (i32, [i32, P, P, P]),
     "mz_log_mel": (i32, [P, u64, P, i32, i32, u64, P]),
+    "mz_tok_open": (i32, [C.c_char_p, i32, i32, C.POINTER(P)]),
+    "mz_tok_from_bytes": (i32, [P, P, i32, C.POINTER(P)]),
+    "mz_tok_free": (i32, [P]),
+    "mz_tok_decode": (i32, [P, P, i32, P, sz, C.POINTER(sz)]),
+    "mz_tok_pieces": (i32, [P, P, P, i32, i32, P, sz, C.POINTER(sz), P, P, P, C.POINTER(i32)]),
+    "mz_json_time": (i32, [f32, P, sz, C.POINTER(sz)]),
+    "mz_results_json": (i32, [P, P, i32, P, P, P, i32, P, P, P, sz, C.POINTER(sz)]),
+    "mz_cli": (i32, [i32, P]),
     "mz_jump_times": (i32, [P, i32, i32, i32, i32, i32, i32, P]),
     "mz_jump_times_device": (i32, [P, u64, C.c_int64, i32, P, P, i32, i32, i32, i32, P, C.c_int64]),
     "mz_dtw": (i32, [P, i32, i32, P, P, P]),

@@ -3,7 +3,9 @@
     python -m mimizuku_amd.build          # or __graft_entry__.build()
 
 Every source under csrc/ is compiled to an object in _build/ (in parallel), then linked into
-mimizuku_amd/libmimizuku_amd.so. Packed fp32 VALU forms are disabled for the device code.
+mimizuku_amd/libmimizuku_amd.so. Packed fp32 VALU forms are disabled for the device code. The command-line tool
+cli/mimizuku.cpp (host code over the C ABI) is linked against the library as mimizuku_amd/mimizuku, which finds
+the library next to itself.
 """
 from __future__ import annotations
 
@@ -16,6 +18,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libmimizuku_amd.so")
+CLI_SRC = os.path.join(HERE, "cli", "mimizuku.cpp")
+CLI_OUT = os.path.join(HERE, "mimizuku")
 BUILD = os.path.join(ROOT, "_build")
 ARCH = os.environ.get("MZ_OFFLOAD_ARCH", "gfx950")
 
@@ -54,8 +58,15 @@ def build(verbose: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, OUT)
+    tmp = CLI_OUT + ".tmp"
+    cmd = [HIPCC, "-O2", "-std=c++17", "-Wno-unused-result", CLI_SRC, "-o", tmp, f"-L{HERE}", "-lmimizuku_amd",
+           "-Wl,-rpath,$ORIGIN", "-lpthread"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"building the command-line tool failed:\n{r.stderr}")
+    os.replace(tmp, CLI_OUT)
     if verbose:
-        print(f"built {OUT}", file=sys.stderr)
+        print(f"built {OUT} and {CLI_OUT}", file=sys.stderr)
     return OUT
 
 
