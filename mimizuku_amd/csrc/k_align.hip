@@ -119,8 +119,14 @@ __global__ void __launch_bounds__(256) ts_cost_kernel(const MzTs p) {
     p.cost[c * p.diag_stride + (long)(i + j + 2) * p.ldd + (i + 1)] = s;
 }
 
-// One workgroup per clip. Row i of the table (0..R) is handled by threads i, i + blockDim, ...
+// One workgroup per clip. Row i of the table (0..R) is handled by threads i, i + blockDim, ... The costs are staged
+// in LDS DTW_CH diagonals at a time (diagonal-major, so a chunk is one contiguous run, copied with direct-to-LDS
+// loads) while the previous chunk is being used; within a chunk a diagonal waits only for the LDS traffic of the
+// one before (lds_barrier), so the trace stores and the next chunk's loads stay in flight.
+constexpr int DTW_CH = 12;
+
 __global__ void __launch_bounds__(1024) ts_dtw_kernel(const MzTs p) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the buffer-resource type exists only in the device pass
     extern __shared__ float lds[];
     const int c = blockIdx.x, R = p.rc[c].x, C = p.rc[c].y, nt = blockDim.x, tid = threadIdx.x;
     float* out = p.out + (long)c * p.out_stride;
@@ -132,43 +138,65 @@ __global__ void __launch_bounds__(1024) ts_dtw_kernel(const MzTs p) {
     const int ld = p.ldd;
     float* diag = lds;                       // 3 x (R + 1): diagonals d, d - 1, d - 2 in rotation
     int* first = (int*)(lds + 3 * ld);       // per row: the column of the path's first cell in that row
+    float* chunk = lds + 4 * ld;             // 2 x DTW_CH diagonals of costs
     const float* cost = p.cost + c * p.diag_stride;
     signed char* tr = p.trace + c * p.diag_stride;
-    for (int d = 0; d <= R + C; d++) {
-        float* cur = diag + (d % 3) * ld;
-        const float* p1 = diag + ((d + 2) % 3) * ld;
-        const float* p2 = diag + ((d + 1) % 3) * ld;
-        const int lo = max(0, d - C), hi = min(R, d);
-        for (int i = lo + tid; i <= hi; i += nt) {
-            const int j = d - i;
-            float v;
-            signed char t;
-            if (i == 0) {
-                v = d == 0 ? 0.f : INFINITY;
-                t = 2;
-            } else if (j == 0) {
-                v = INFINITY;
-                t = 1;
-            } else {
-                const float c0 = p2[i - 1], c1 = p1[i - 1], c2 = p1[i];
-                float m;
-                if (c0 < c1 && c0 < c2) {
-                    m = c0;
-                    t = 0;
-                } else if (c1 < c0 && c1 < c2) {
-                    m = c1;
+    // reads past the clip's cost table return zeros (the descriptor's range check)
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(cost), (short)0,
+                                                                         (int)(p.diag_stride * 4), 0x00020000);
+    // a chunk buffer holds a whole number of 64-float wave copies (the last one may read past the chunk)
+    const int lane = tid & 63, wave = tid >> 6, per = (DTW_CH * ld + 63) & ~63;
+    auto stage = [&](int d0, float* dst) {
+        // wave w's lanes copy floats w * 64 + lane, + nt, ... of diagonals d0 .. d0 + DTW_CH - 1
+        for (int k = wave * 64; k < per; k += nt)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (__attribute__((address_space(3))) void*)(dst + k), 4,
+                                                     (unsigned)((d0 * ld + k + lane) * 4), 0, 0, 0);
+    };
+    stage(0, chunk);
+    for (int d0 = 0; d0 <= R + C; d0 += DTW_CH) {
+        float* cb = chunk + ((d0 / DTW_CH) & 1) * per;
+        __builtin_amdgcn_s_waitcnt(0);  // this chunk's copies (and the trace stores so far) are done
+        __syncthreads();                // ... in every wave, and the other buffer's last chunk is no longer read
+        if (d0 + DTW_CH <= R + C) stage(d0 + DTW_CH, chunk + (((d0 / DTW_CH) + 1) & 1) * per);
+        const int dend = min(d0 + DTW_CH, R + C + 1);
+        for (int d = d0; d < dend; d++) {
+            float* cur = diag + (d % 3) * ld;
+            const float* p1 = diag + ((d + 2) % 3) * ld;
+            const float* p2 = diag + ((d + 1) % 3) * ld;
+            const float* cd = cb + (d - d0) * ld;
+            const int lo = max(0, d - C), hi = min(R, d);
+            for (int i = lo + tid; i <= hi; i += nt) {
+                const int j = d - i;
+                float v;
+                signed char t;
+                if (i == 0) {
+                    v = d == 0 ? 0.f : INFINITY;
+                    t = 2;
+                } else if (j == 0) {
+                    v = INFINITY;
                     t = 1;
                 } else {
-                    m = c2;
-                    t = 2;
+                    const float c0 = p2[i - 1], c1 = p1[i - 1], c2 = p1[i];
+                    float m;
+                    if (c0 < c1 && c0 < c2) {
+                        m = c0;
+                        t = 0;
+                    } else if (c1 < c0 && c1 < c2) {
+                        m = c1;
+                        t = 1;
+                    } else {
+                        m = c2;
+                        t = 2;
+                    }
+                    v = (float)(-(double)cd[i] + (double)m);
                 }
-                v = (float)(-(double)cost[(long)d * ld + i] + (double)m);
+                cur[i] = v;
+                tr[(long)d * ld + i] = t;
             }
-            cur[i] = v;
-            tr[(long)d * ld + i] = t;
+            lds_barrier();
         }
-        __syncthreads();
     }
+    __builtin_amdgcn_s_waitcnt(0);
     // the trace stores went to global memory from every lane: make them visible to the walking lane
     __threadfence_block();
     __syncthreads();
@@ -192,11 +220,13 @@ __global__ void __launch_bounds__(1024) ts_dtw_kernel(const MzTs p) {
         const int r0 = row0 ? 0 : 1;
         for (int n = 0; n < R; n++) out[n] = (float)((double)first[r0 + n] * 0.02);
     }
+#endif
 }
 
 }  // namespace
 
-size_t mz_ts_lds_bytes(int rmax) { return (size_t)(rmax + 1) * 4 * 4; }
+// 3 diagonals, the first-column table and 2 chunks of DTW_CH diagonals of costs, ld = rmax + 1 floats each
+size_t mz_ts_lds_bytes(int rmax) { return ((size_t)(rmax + 1) * 4 + 2 * (((size_t)DTW_CH * (rmax + 1) + 63) & ~(size_t)63)) * 4; }
 
 hipError_t mz_ts_launch(hipStream_t s, const MzTs& p, int n) {
     if (n <= 0) return hipSuccess;
@@ -214,6 +244,7 @@ hipError_t mz_ts_launch(hipStream_t s, const MzTs& p, int n) {
     }
     int nt = ((p.rmax + 1 + 63) / 64) * 64;
     nt = nt < 256 ? 256 : nt > 1024 ? 1024 : nt;
+    if (mz_ts_lds_bytes(p.ldd - 1) > 64 * 1024 || p.diag_stride * 4 >= (1L << 31)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(ts_dtw_kernel, dim3(n), dim3(nt), mz_ts_lds_bytes(p.ldd - 1), s, p);
     return hipGetLastError();
 }

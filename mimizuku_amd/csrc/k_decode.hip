@@ -129,11 +129,6 @@ constexpr int MZ_NT = 2;  // cache-policy bit of a buffer load: nontemporal (wei
 // Workgroup barrier that waits for this wave's LDS operations only, not for its loads in flight (a __syncthreads
 // would also wait for every outstanding global load); the memory clobber keeps the compiler from moving LDS
 // accesses across it.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt and expcnt unconstrained
-    asm volatile("s_barrier" ::: "memory");
-}
-
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigned bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }

@@ -52,6 +52,13 @@ __device__ __forceinline__ float gelu_erf(float v) {
     return 0.5f * v * (v >= 0.f ? 2.f - q : q);
 }
 
+// A workgroup barrier for LDS traffic only: waits for this wave's LDS operations (lgkmcnt(0)) but not for its
+// global loads and stores, which __syncthreads would drain (its vmcnt(0)), so loads issued ahead stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt and expcnt unconstrained
+    asm volatile("s_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ f16x8 ld8(const f16* p) { return *(const f16x8*)p; }
 __device__ __forceinline__ void st4(f16* p, float a, float b, float c, float d) {
     f16x4 v = {(f16)a, (f16)b, (f16)c, (f16)d};
