@@ -11,7 +11,7 @@
 //   mel_dft_kernel    one workgroup per (16 frames, clip): the frames' 2,800 samples staged in LDS, thread k < 201
 //                     owns bin k of the 16 frames (32 double accumulators), the basis read sample-major so a
 //                     wave's loads are contiguous
-//   mel_filter_kernel one thread per (mel, frame): the filter sum and the log
+//   mel_filter_kernel one workgroup per (frame, clip): the frame's power spectrum in LDS, one thread per mel
 //   mel_norm_kernel   one workgroup per clip: the maximum, then the clamp and scale in place
 #include <math.h>
 
@@ -30,7 +30,7 @@ __device__ __forceinline__ int live_frames(int n) {
 }
 
 __global__ void __launch_bounds__(256) mel_dft_kernel(const MzMel p) {
-    __shared__ float xs[SPAN];
+    __shared__ __attribute__((aligned(16))) float xs[SPAN];
     const int c = blockIdx.y, t0 = blockIdx.x * FB, n = p.ns[c];
     if (t0 >= live_frames(n)) return;
     const float* y = p.audio + (long)c * MZ_MEL_NSAMPLES;
@@ -47,13 +47,24 @@ __global__ void __launch_bounds__(256) mel_dft_kernel(const MzMel p) {
     double re[FB], im[FB];
 #pragma unroll
     for (int f = 0; f < FB; f++) re[f] = im[f] = 0.0;
-    for (int j = 0; j < MZ_MEL_NFFT; j++) {
-        const double cj = p.cosb[j * MZ_MEL_BINS + k], sj = p.sinb[j * MZ_MEL_BINS + k];
+    // four samples per step: one 16-byte LDS read per frame, the sums still taken one sample at a time
+    for (int j = 0; j < MZ_MEL_NFFT; j += 4) {
+        double cj[4], sj[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            cj[q] = p.cosb[(j + q) * MZ_MEL_BINS + k];
+            sj[q] = p.sinb[(j + q) * MZ_MEL_BINS + k];
+        }
 #pragma unroll
         for (int f = 0; f < FB; f++) {
-            const double x = (double)xs[f * MZ_MEL_HOP + j];
-            re[f] = re[f] + x * cj;
-            im[f] = im[f] + x * sj;
+            const float4 x4 = *(const float4*)&xs[f * MZ_MEL_HOP + j];
+            const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const double x = (double)xv[q];
+                re[f] = re[f] + x * cj[q];
+                im[f] = im[f] + x * sj[q];
+            }
         }
     }
     const int live = live_frames(n);
@@ -65,16 +76,22 @@ __global__ void __launch_bounds__(256) mel_dft_kernel(const MzMel p) {
 }
 
 __global__ void __launch_bounds__(256) mel_filter_kernel(const MzMel p) {
-    const int c = blockIdx.z, m = blockIdx.y, t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= MZ_NFR_HOST) return;
-    float v = -10.f;
-    if (t < live_frames(p.ns[c])) {
-        const float* pw = p.pow + ((long)c * MZ_NFR_HOST + t) * MZ_MEL_BINS;
-        float acc = 0.f;
-        for (int k = 0; k < MZ_MEL_BINS; k++) acc = acc + p.filt[k * p.n_mels + m] * pw[k];
-        v = log10f(fmaxf(acc, 1e-10f));
+    __shared__ float pw[MZ_MEL_BINS];
+    const int c = blockIdx.y, t = blockIdx.x;
+    const bool live = t < live_frames(p.ns[c]);
+    if (live)
+        for (int k = threadIdx.x; k < MZ_MEL_BINS; k += blockDim.x)
+            pw[k] = p.pow[((long)c * MZ_NFR_HOST + t) * MZ_MEL_BINS + k];
+    __syncthreads();
+    for (int m = threadIdx.x; m < p.n_mels; m += blockDim.x) {
+        float v = -10.f;
+        if (live) {
+            float acc = 0.f;
+            for (int k = 0; k < MZ_MEL_BINS; k++) acc = acc + p.filt[k * p.n_mels + m] * pw[k];
+            v = log10f(fmaxf(acc, 1e-10f));
+        }
+        p.mel[((long)c * p.n_mels + m) * MZ_NFR_HOST + t] = v;
     }
-    p.mel[((long)c * p.n_mels + m) * MZ_NFR_HOST + t] = v;
 }
 
 __global__ void __launch_bounds__(1024) mel_norm_kernel(const MzMel p) {
@@ -99,7 +116,7 @@ __global__ void __launch_bounds__(1024) mel_norm_kernel(const MzMel p) {
 hipError_t mz_log_mel_launch(hipStream_t s, const MzMel& p) {
     if (p.n <= 0 || p.n_mels <= 0 || p.n_mels > 65535) return hipErrorInvalidValue;
     hipLaunchKernelGGL(mel_dft_kernel, dim3((MZ_NFR_HOST + FB - 1) / FB, p.n), dim3(256), 0, s, p);
-    hipLaunchKernelGGL(mel_filter_kernel, dim3((MZ_NFR_HOST + 255) / 256, p.n_mels, p.n), dim3(256), 0, s, p);
+    hipLaunchKernelGGL(mel_filter_kernel, dim3(MZ_NFR_HOST, p.n), dim3(p.n_mels <= 128 ? 128 : 256), 0, s, p);
     hipLaunchKernelGGL(mel_norm_kernel, dim3(p.n), dim3(1024), 0, s, p);
     return hipGetLastError();
 }
