@@ -168,7 +168,8 @@ int mz_engine_step(mz_engine* e, int b, int lang, int prompt_len);
 /* Capture step(b, 0, prompt_len) once as a graph and upload it; replay launches it (transcribe.rs:123-142). */
 int mz_engine_capture(mz_engine* e, int b, int prompt_len);
 int mz_engine_replay(mz_engine* e);
-/* Keep a copy of every encoder layer's input (fp32 residual stream) of the next encode (Engine::trace). */
+/* Keep a copy of every encoder layer's input (fp32 residual stream) of the next encode (Engine::trace), and of the
+ * decoder residual entering every layer of each eager step (MZ_BUF_DEC_TRACE). */
 int mz_engine_set_trace(mz_engine* e, int on);
 
 /* Kernel timing (the reference's stage timings, src/main.rs:213-222, at kernel granularity): with profiling on, every
@@ -198,6 +199,10 @@ int mz_engine_profile_read(mz_engine* e, int kernel, double* total_ms, int* coun
 #define MZ_BUF_XKV 7     /* f16 [bmax][dec_layers][2][nh] tiles of 1536 x 64 (k, v as [t][64]) */
 #define MZ_BUF_DEC_X 8   /* f32 [bmax][d] decoder residual stream */
 #define MZ_BUF_ENC_X 9   /* f32 [eg * 1500][d] encoder residual stream */
+#define MZ_BUF_DEC_TRACE 10 /* f32 [dec_layers + 1][bmax][d]: with the trace on, the decoder residual entering each
+                             * layer and after the last one, of the last eager step (not recorded by graph replays) */
+#define MZ_BUF_SELF_K 11 /* f16 [dec_layers][bmax][nh][max_t][64] self-attention key cache */
+#define MZ_BUF_SELF_V 12 /* f16 [dec_layers][bmax][nh][max_t][64] self-attention value cache */
 /* Device address and size of an engine buffer. */
 int mz_engine_buffer(mz_engine* e, int which, uint64_t* dptr, size_t* bytes);
 /* Synchronise, then copy bytes at byte offset `offset` of an engine buffer to host memory. */

@@ -69,6 +69,7 @@ struct mz_engine {
     int sot = 0, eos = 0, bs1 = -1, bs2 = -1;
     std::vector<int> align_heads;  // pairs
     bool trace_on = false;
+    bool capturing = false;  // inside mz_engine_capture: no trace copies go into the graph
     bool loaded = false;
 
     // weights
@@ -90,6 +91,7 @@ struct mz_engine {
     f16 *melT = nullptr, *h1 = nullptr, *hb = nullptr, *qkvh = nullptr, *att = nullptr, *ff = nullptr;
     f16* dd = nullptr;  // out-projection / fc2 output, added to the residual stream by the next add + LayerNorm
     float *ex = nullptr, *trace = nullptr;
+    float* dtrace = nullptr;  // decoder residual entering every layer and after the last, [nl + 1][bmax][d]
     // more encoder lanes for batches of several groups: each with its own scratch and stream, so that one group's
     // bandwidth-bound kernels and kernel tails overlap another's products (the groups are independent)
     EncBufs lanes[MZ_ENC_LANES - 1]{};
@@ -428,6 +430,7 @@ extern "C" int mz_engine_set_trace(mz_engine* e, int on) {
     if (!e) return mz_fail(MZ_ERR_ARG, "mz_engine_set_trace: null engine");
     if (on && !e->trace) {
         if (int r = e->alloc(&e->trace, (size_t)e->dm.enc_layers * e->eg * TENC * e->dm.d)) return r;
+        if (int r = e->alloc(&e->dtrace, (size_t)(e->dm.dec_layers + 1) * e->bmax * e->dm.d)) return r;
     }
     e->trace_on = on != 0;
     return MZ_OK;
@@ -646,6 +649,12 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
     TRY(mz_dec_embed_ln_launch(s, e->tok, e->ctr, e->emb, e->dpos, e->x, e->decv[0].ln1.w, e->decv[0].ln1.b, e->h, b, D,
                                mt, EPS),
         "embed");
+    // with the trace on (eager steps only): the residual entering layer l, l = 0 .. nl (nl: after the last layer)
+    const bool dtr = e->trace_on && e->dtrace && !e->capturing;
+    auto dtrace = [&](int l) {
+        return hipMemcpyAsync(e->dtrace + (size_t)l * e->bmax * D, e->x, (size_t)b * D * 4, hipMemcpyDeviceToDevice, s);
+    };
+    if (dtr) TRY(dtrace(0), "decoder trace");
     auto gemm = [&](int epi, const f16* x, int ldx, const Lin& L, int N, int K, int ks, void* out, long ldo) {
         MzDec g{};
         g.x = x;
@@ -722,6 +731,7 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
         TRY(gemm(DEPI_PARTIAL, e->dff, F, L.fc2, D, F, ks_df, e->part, D), "dec fc2");
         const Ln& nx = i + 1 < nl ? e->decv[i + 1].ln1 : e->dln;
         TRY(mz_dec_add_ln_launch(s, e->x, e->part, ks_df, (long)b * D, L.fc2.b, nx.w, nx.b, e->h, b, D, EPS), "add+ln");
+        if (dtr) TRY(dtrace(i + 1), "decoder trace");
     }
     // tied LM head with the masked per-workgroup argmax, then the greedy choice, which advances the position
     {
@@ -776,7 +786,9 @@ extern "C" int mz_engine_capture(mz_engine* e, int b, int prompt_len) {
     if (int r = mz_graph_begin(e->c)) return r;
     const bool prof = e->prof_on;
     e->prof_on = false;  // events are not recorded into the graph
+    e->capturing = true;
     int rs = step_impl(e, b, 0, prompt_len);
+    e->capturing = false;
     e->prof_on = prof;
     mz_graph* g = nullptr;
     int re = mz_graph_end(e->c, &g);
@@ -818,6 +830,12 @@ extern "C" int mz_engine_buffer(mz_engine* e, int which, uint64_t* dptr, size_t*
         case MZ_BUF_XKV: p = e->xkvbuf, n = B * e->dm.dec_layers * 2 * e->dm.nh * (size_t)TPAD * HD * 2; break;
         case MZ_BUF_DEC_X: p = e->x, n = B * D * 4; break;
         case MZ_BUF_ENC_X: p = e->ex, n = G * TENC * D * 4; break;
+        case MZ_BUF_DEC_TRACE:
+            if (!e->dtrace) return mz_fail(MZ_ERR_STATE, "trace not enabled");
+            p = e->dtrace, n = (size_t)(e->dm.dec_layers + 1) * B * D * 4;
+            break;
+        case MZ_BUF_SELF_K: p = e->kc, n = (size_t)e->dm.dec_layers * B * e->dm.nh * e->dm.max_t * HD * 2; break;
+        case MZ_BUF_SELF_V: p = e->vc, n = (size_t)e->dm.dec_layers * B * e->dm.nh * e->dm.max_t * HD * 2; break;
         default: return mz_fail(MZ_ERR_ARG, "unknown engine buffer %d", which);
     }
     *dptr = (uint64_t)(uintptr_t)p;
@@ -858,7 +876,7 @@ extern "C" int mz_engine_free(mz_engine* e) {
                     (void*)e->ts_out})
         if (p) mz_free(e->c, (uint64_t)(uintptr_t)p);
     for (void* p : {(void*)e->arena, (void*)e->mel, (void*)e->melT, (void*)e->h1, (void*)e->ex, (void*)e->hb, (void*)e->dd,
-                    (void*)e->qkvh, (void*)e->att, (void*)e->ff, (void*)e->trace, (void*)e->xkvbuf, (void*)e->tok,
+                    (void*)e->qkvh, (void*)e->att, (void*)e->ff, (void*)e->trace, (void*)e->dtrace, (void*)e->xkvbuf, (void*)e->tok,
                     (void*)e->done, (void*)e->ctr, (void*)e->x, (void*)e->q, (void*)e->h, (void*)e->datt,
                     (void*)e->dff, (void*)e->kc, (void*)e->vc, (void*)e->logits, (void*)e->align, (void*)e->amax,
                     (void*)e->aslot, (void*)e->sup, (void*)e->sup_lang,

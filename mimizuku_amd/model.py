@@ -349,3 +349,17 @@ class Engine:
 
     def dec_x(self) -> np.ndarray:
         return self.read(L.BUF_DEC_X, np.float32, (self.bmax, self.dims.d))
+
+    def dec_trace(self) -> np.ndarray:
+        """[dec_layers + 1][bmax][d] fp32 decoder residual entering every layer (and after the last) of the last
+        eager step (set_trace first)."""
+        return self.read(L.BUF_DEC_TRACE, np.float32, (self.dims.dec_layers + 1, self.bmax, self.dims.d))
+
+    def self_kv(self) -> tuple[np.ndarray, np.ndarray]:
+        """Self-attention caches, fp16 [dec_layers][bmax][nh][max_t][64] each (keys, values)."""
+        shp = (self.dims.dec_layers, self.bmax, self.dims.nh, self.dims.max_t, 64)
+        return self.read(L.BUF_SELF_K, np.float16, shp), self.read(L.BUF_SELF_V, np.float16, shp)
+
+    def xkv(self) -> np.ndarray:
+        """Cross-attention keys / values of every decoder layer, fp16 [bmax][dec_layers][2][nh][1536][64]."""
+        return self.read(L.BUF_XKV, np.float16, (self.bmax, self.dims.dec_layers, 2, self.dims.nh, 1536, 64))

@@ -168,37 +168,52 @@ class Decoder:
         x = np.stack([emb[t] + pe[p] for t in toks])  # [B, d]
         probs = np.zeros((len(toks), self.nl, nh, TENC), np.float32)
         for i in range(self.nl):
-            pr = f"model.decoder.layers.{i}"
-            h = layer_norm(x, W[f"{pr}.self_attn_layer_norm.weight"], W[f"{pr}.self_attn_layer_norm.bias"])
-            sa = f"{pr}.self_attn"
-            q = linear(h, W[f"{sa}.q_proj.weight"], W[f"{sa}.q_proj.bias"])
-            k = linear(h, W[f"{sa}.k_proj.weight"])
-            v = linear(h, W[f"{sa}.v_proj.weight"], W[f"{sa}.v_proj.bias"])
-            att = np.zeros_like(q)
+            cache = [(_heads(np.stack(self.kc[b][i]), nh) if self.kc[b][i] else None,
+                      _heads(np.stack(self.vc[b][i]), nh) if self.vc[b][i] else None) for b in range(len(toks))]
+            x, k, v, probs[:, i] = decoder_layer(x, W, i, nh, cache, [self.xkv[b][i] for b in range(len(toks))])
             for b in range(len(toks)):
                 self.kc[b][i].append(k[b])
                 self.vc[b][i].append(v[b])
-                K = _heads(np.stack(self.kc[b][i]), nh)
-                V = _heads(np.stack(self.vc[b][i]), nh)
-                o = attention(_heads(q[b:b + 1], nh), K, V)
-                att[b] = _merge(o)[0]
-            x = x + linear(att, W[f"{sa}.out_proj.weight"], W[f"{sa}.out_proj.bias"])
-            h = layer_norm(x, W[f"{pr}.encoder_attn_layer_norm.weight"], W[f"{pr}.encoder_attn_layer_norm.bias"])
-            ca = f"{pr}.encoder_attn"
-            q = linear(h, W[f"{ca}.q_proj.weight"], W[f"{ca}.q_proj.bias"])
-            att = np.zeros_like(q)
-            for b in range(len(toks)):
-                K, V = self.xkv[b][i]
-                o, pb = attention(_heads(q[b:b + 1], nh), K, V, return_probs=True)
-                att[b] = _merge(o)[0]
-                probs[b, i] = pb[:, 0, :]
-            x = x + linear(att, W[f"{ca}.out_proj.weight"], W[f"{ca}.out_proj.bias"])
-            h = layer_norm(x, W[f"{pr}.final_layer_norm.weight"], W[f"{pr}.final_layer_norm.bias"])
-            f = gelu(linear(h, W[f"{pr}.fc1.weight"], W[f"{pr}.fc1.bias"]))
-            x = x + linear(f, W[f"{pr}.fc2.weight"], W[f"{pr}.fc2.bias"])
         h = layer_norm(x, W["model.decoder.layer_norm.weight"], W["model.decoder.layer_norm.bias"])
         logits = linear(h, W["model.decoder.embed_tokens.weight"])
         return logits, probs
+
+
+def decoder_layer(x: np.ndarray, W: dict, i: int, nh: int, cache: list, xkv: list):
+    """One WhisperDecoderLayer for one new position of B rows (TF/modeling_whisper.py:469-503): x [B][d] the residual
+    entering the layer; cache[b] = (K, V) [nh][p][64] of the earlier positions of row b (None at position 0);
+    xkv[b] = (K, V) [nh][1500][64] of the encoder. Returns the residual after the layer, the new key and value rows
+    [B][d] and the cross-attention probabilities [B][nh][1500]."""
+    pr = f"model.decoder.layers.{i}"
+    B = x.shape[0]
+    h = layer_norm(x, W[f"{pr}.self_attn_layer_norm.weight"], W[f"{pr}.self_attn_layer_norm.bias"])
+    sa = f"{pr}.self_attn"
+    q = linear(h, W[f"{sa}.q_proj.weight"], W[f"{sa}.q_proj.bias"])
+    k = linear(h, W[f"{sa}.k_proj.weight"])
+    v = linear(h, W[f"{sa}.v_proj.weight"], W[f"{sa}.v_proj.bias"])
+    att = np.zeros_like(q)
+    for b in range(B):
+        K, V = _heads(k[b:b + 1], nh), _heads(v[b:b + 1], nh)
+        if cache[b][0] is not None:
+            K = np.concatenate([cache[b][0], K], 1)
+            V = np.concatenate([cache[b][1], V], 1)
+        att[b] = _merge(attention(_heads(q[b:b + 1], nh), K, V))[0]
+    x = x + linear(att, W[f"{sa}.out_proj.weight"], W[f"{sa}.out_proj.bias"])
+    h = layer_norm(x, W[f"{pr}.encoder_attn_layer_norm.weight"], W[f"{pr}.encoder_attn_layer_norm.bias"])
+    ca = f"{pr}.encoder_attn"
+    q = linear(h, W[f"{ca}.q_proj.weight"], W[f"{ca}.q_proj.bias"])
+    att = np.zeros_like(q)
+    probs = np.zeros((B, nh, TENC), np.float32)
+    for b in range(B):
+        K, V = xkv[b]
+        o, pb = attention(_heads(q[b:b + 1], nh), K, V, return_probs=True)
+        att[b] = _merge(o)[0]
+        probs[b] = pb[:, 0, :]
+    x = x + linear(att, W[f"{ca}.out_proj.weight"], W[f"{ca}.out_proj.bias"])
+    h = layer_norm(x, W[f"{pr}.final_layer_norm.weight"], W[f"{pr}.final_layer_norm.bias"])
+    f = gelu(linear(h, W[f"{pr}.fc1.weight"], W[f"{pr}.fc1.bias"]))
+    x = x + linear(f, W[f"{pr}.fc2.weight"], W[f"{pr}.fc2.bias"])
+    return x, k, v, probs
 
 
 def choose(logits: np.ndarray, suppress, begin_suppress, first: bool, eos: int, done: bool) -> int:

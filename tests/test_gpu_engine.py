@@ -126,6 +126,40 @@ def test_decoder_teacher_forced(ctx, case):
     e.close()
 
 
+def test_decoder_layer_local(ctx, case):
+    """Every decoder layer layer-local at every teacher-forced position: the oracle's layer applied to the engine's own
+    fp32 residual entering it, with the engine's own (fp16) self-attention cache of the earlier positions and its
+    cross keys / values, against the residual the engine produced, max-abs <= 2e-3 x RMS; the new cache rows
+    against the oracle's k / v within fp16 rounding."""
+    e = case.engine(ctx)
+    e.set_trace(True)
+    e.encode(case.mel, 0)
+    seq = case.seq.astype(np.int32)
+    T = seq.shape[1]
+    e.reset(seq)
+    n, nh, nl = case.n, G.nh, G.dec_layers
+    xkv = e.xkv()[:n].astype(np.float32)
+    worst = worst_kv = 0.0
+    for p in range(T - 1):
+        e.step(n, False, T)
+        tr = e.dec_trace()[:, :n]
+        kc, vc = e.self_kv()
+        for i in range(nl):
+            cache = [(kc[i, b, :, :p].astype(np.float32), vc[i, b, :, :p].astype(np.float32)) if p else (None, None)
+                     for b in range(n)]
+            cross = [(xkv[b, i, 0, :, :1500], xkv[b, i, 1, :, :1500]) for b in range(n)]
+            out, k, v, _ = R.decoder_layer(tr[i], case.Wf, i, nh, cache, cross)
+            err = rel_err(tr[i + 1], out)
+            worst = max(worst, err)
+            assert err <= TOL, (p, i, err)
+            for got, ref in ((kc[i, :n, :, p], k), (vc[i, :n, :, p], v)):
+                ref = ref.reshape(n, nh, 64)
+                worst_kv = max(worst_kv, float(np.abs(got.astype(np.float32) - ref).max() / np.sqrt((ref ** 2).mean())))
+    print(case.name, "decoder layer-local max-abs / RMS", worst, "new k/v", worst_kv)
+    assert worst_kv <= TOL
+    e.close()
+
+
 def test_transcribe_matches_golden(ctx, case):
     e = case.engine(ctx)
     p = transcribe.Prompt(e.gc, "auto" if case.detect else "en")
