@@ -17,6 +17,9 @@ top-2 margin exceeds 1e-2. Bars as in test_gpu_engine.py, except the alignment r
 largest probability. These rows are nearly uniform (the largest ~0.01), and each probability carries the relative
 error of its score, ~1e-3 here from the fp16 rounding of the LayerNorm output that feeds the query (the oracle keeps
 it in fp32; the reference rounds it, as this build does).
+
+At the benchmark's own positions (200 .. 203, the self-attention cache holding 200+ keys) every decoder layer is
+checked layer-local on the engine's residual trace, and the logits of its final residual against the oracle's head.
 """
 import numpy as np
 import pytest
@@ -115,5 +118,52 @@ def test_decoder_turbo_widths_batch32():
     print("turbo widths, B = 32: logits max-abs / RMS", worst, "; greedy choices checked", checked)
     assert worst < 2e-2
     assert checked >= B // 2
+    e.close()
+    ctx.close()
+
+
+def test_decoder_turbo_widths_at_position_200():
+    """The benchmark's decoder step shape: 32 rows at positions 200 .. 203, the self-attention cache holding 200+
+    keys. Every decoder layer layer-local (the oracle's layer on the engine's own residual, cache and cross
+    keys / values) within 2e-3 x RMS, and the logits of the engine's final residual within 2e-2 x RMS."""
+    rng = np.random.default_rng(22)
+    W = synth.random_weights(G, seed=6, bias_std=0.02, ln_std=0.1)
+    Wf = {k: v.astype(np.float32) for k, v in W.items() if k.startswith("model.decoder")}
+    gen = synth.generation_config(G, align_heads=[[2, 4], [2, 11], [3, 3], [3, 6], [3, 11], [3, 14]])
+    dims = model.Dims(G.d, G.ff, G.nh, G.enc_layers, G.dec_layers, G.n_mels, G.vocab, G.max_t)
+    gc = model.GenCfg.from_dict(gen, dims)
+    xkv = np.zeros((B, G.dec_layers, 2, G.nh, TPAD, 64), np.float16)
+    for b in range(B):
+        xkv[b, :, :, :, :1500] = rng.standard_normal((G.dec_layers, 2, G.nh, 1500, 64), dtype=np.float32)
+    npr = 204
+    prompts = rng.integers(0, 50000, size=(B, npr)).astype(np.int32)
+    ctx = model.Context(0)
+    e = model.Engine(ctx, dims, gc, B, 8)
+    e.load(W)
+    e.set_trace(True)
+    p, _ = e.buffer(L.BUF_XKV)
+    ctx.upload(p, xkv)
+    cross = [[(xkv[b, i, 0, :, :1500].astype(np.float32), xkv[b, i, 1, :, :1500].astype(np.float32))
+              for b in range(B)] for i in range(G.dec_layers)]
+    del xkv
+    e.reset(prompts)
+    worst = worst_lg = 0.0
+    for pos in range(npr):
+        e.step(B, False, npr)
+        if pos < 200:
+            continue
+        tr = e.dec_trace()[:, :B]
+        kc, vc = e.self_kv()
+        for i in range(G.dec_layers):
+            cache = [(kc[i, b, :, :pos].astype(np.float32), vc[i, b, :, :pos].astype(np.float32)) for b in range(B)]
+            out, _, _, _ = R.decoder_layer(tr[i], Wf, i, G.nh, cache, cross[i])
+            err = rel_err(tr[i + 1], out)
+            worst = max(worst, err)
+            assert err <= 2e-3, (pos, i, err)
+        h = R.layer_norm(tr[-1], Wf["model.decoder.layer_norm.weight"], Wf["model.decoder.layer_norm.bias"])
+        ref = R.linear(h, Wf["model.decoder.embed_tokens.weight"])
+        worst_lg = max(worst_lg, rel_err(e.logits()[:B], ref))
+    print("turbo widths, B = 32, positions 200..203: layer-local max-abs / RMS", worst, "; logits", worst_lg)
+    assert worst_lg < 2e-2
     e.close()
     ctx.close()
