@@ -220,15 +220,7 @@ __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
                 }
             }
         }
-#pragma unroll
-        for (int o = 1; o < 8; o <<= 1) {  // the 8 lanes of one row are adjacent in the wave
-            const float ov = __shfl_xor(best, o);
-            const int oi = __shfl_xor(bi, o);
-            if (ov > best || (ov == best && oi < bi)) {
-                best = ov;
-                bi = oi;
-            }
-        }
+        group8_argmax(best, bi);  // the 8 lanes of one row are adjacent in the wave
         if ((tid & 7) == 0 && m < p.M) {
             int2 r;
             r.x = __float_as_int(best);
@@ -395,15 +387,7 @@ __global__ void __launch_bounds__(256) dec_lmhead_kernel(const MzDec p, int T) {
             }
         }
     }
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) {  // the 8 threads of one row are adjacent lanes
-        const float ov = __shfl_xor(best, o);
-        const int oi = __shfl_xor(bi, o);
-        if (ov > best || (ov == best && oi < bi)) {
-            best = ov;
-            bi = oi;
-        }
-    }
+    group8_argmax(best, bi);  // the 8 threads of one row are adjacent lanes
     if ((tid & 7) == 0 && em < p.M) {
         int2 r;
         r.x = __float_as_int(best);
@@ -470,9 +454,7 @@ __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
             float t = 0.f;
 #pragma unroll
             for (int e = 0; e < 8; e++) t = fmaf(q8[e], (float)kk[u][e], t);
-            t += __shfl_xor(t, 1);
-            t += __shfl_xor(t, 2);
-            t += __shfl_xor(t, 4);
+            t = group8_sum(t);
             const int j = j0 + u * AG;
             s[u] = j < L ? t : -INFINITY;
             if (slot >= 0 && sub == 0 && j < L) sc[j] = t;
@@ -555,15 +537,7 @@ __global__ void __launch_bounds__(256) dec_argmax_kernel(const int2* __restrict_
             }
         }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(best, o);
-        const int oi = __shfl_xor(bi, o);
-        if (ov > best || (ov == best && oi < bi)) {
-            best = ov;
-            bi = oi;
-        }
-    }
+    wave_argmax(best, bi);
     if ((tid & 63) == 0) {
         sv[tid >> 6] = best;
         si[tid >> 6] = bi;

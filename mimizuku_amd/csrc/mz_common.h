@@ -27,15 +27,80 @@ __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Cross-lane moves through DPP: a vector-ALU operand modifier of a few cycles, where __shfl_xor becomes an LDS
+// permute (a round trip through the LDS pipeline). Controls (GCN / CDNA): quad_perm [1,0,3,2] = 0xB1 (lane ^ 1),
+// [2,3,0,1] = 0x4E (lane ^ 2), row_half_mirror = 0x141 (lane i of 8 reads 7 - i), row_mirror = 0x140 (lane i of 16
+// reads 15 - i). Every lane of the groups involved must be active.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+// sum over each aligned group of 8 lanes, in every lane of the group
+__device__ __forceinline__ float group8_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    return v + dpp_f<0x141>(v);
+}
+// sum / max over the wave, in every lane: 16-lane rows through DPP, then the four row values through lane reads
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v = group8_sum(v);
+    v += dpp_f<0x140>(v);
+    const int b = __builtin_bit_cast(int, v);
+    return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+           (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
 }
 __device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    const int b = __builtin_bit_cast(int, v);
+    return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))),
+                 fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48))));
+}
+// (value, index) maximum over each aligned group of 8 lanes, ties to the lowest index, in every lane of the group
+__device__ __forceinline__ void group8_argmax(float& best, int& bi) {
+    auto step = [&](float ov, int oi) {
+        if (ov > best || (ov == best && oi < bi)) {
+            best = ov;
+            bi = oi;
+        }
+    };
+    step(dpp_f<0xB1>(best), dpp_i<0xB1>(bi));
+    step(dpp_f<0x4E>(best), dpp_i<0x4E>(bi));
+    step(dpp_f<0x141>(best), dpp_i<0x141>(bi));
+}
+// the same over the whole wave (every lane active), in every lane
+__device__ __forceinline__ void wave_argmax(float& best, int& bi) {
+    group8_argmax(best, bi);
+    const float ov = dpp_f<0x140>(best);
+    const int oi = dpp_i<0x140>(bi);
+    if (ov > best || (ov == best && oi < bi)) {
+        best = ov;
+        bi = oi;
+    }
+    const int fb = __builtin_bit_cast(int, best);
+    float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(fb, 0));
+    int i = __builtin_amdgcn_readlane(bi, 0);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    for (int r = 16; r < 64; r += 16) {
+        const float rv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(fb, r));
+        const int ri = __builtin_amdgcn_readlane(bi, r);
+        if (rv > b || (rv == b && ri < i)) {
+            b = rv;
+            i = ri;
+        }
+    }
+    best = b;
+    bi = i;
 }
 
 // Exact (erf) GELU, as nn.GELU(): 0.5 v (1 + erf(v / sqrt 2)), with erf from Abramowitz & Stegun 7.1.26 (Hastings'
