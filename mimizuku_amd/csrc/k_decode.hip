@@ -141,13 +141,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigne
 // 16-byte position c ^ r ^ (rg & 1): the fragment reads of 16 consecutive lanes (8 rows of two blocks) hit distinct
 // banks. The 4 waves split the K groups; their 32x32 products are summed in LDS. Every operand of the epilogue (bias,
 // mask, position) is requested at entry with the loads, so the kernel makes a single round trip to memory.
-template <int EPI>
+// KS: the largest K slice of the launch (LDS sized to it: a workgroup asks for no more than it uses)
+template <int EPI, int KS>
 __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the buffer-resource type exists only in the device pass
     constexpr int NC = 4;  // output columns per epilogue thread
-    __shared__ __attribute__((aligned(16))) f16 lds[64 * MZ_DEC_KSLICE];
+    static_assert(KS <= MZ_DEC_KSLICE && 64 * KS * 2 >= 4 * 32 * 33 * 4, "LDS holds the operands and the reduction");
+    __shared__ __attribute__((aligned(16))) f16 lds[64 * KS];
     f16* const sw = lds;
-    f16* const sx = lds + 32 * MZ_DEC_KSLICE;
+    f16* const sx = lds + 32 * KS;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, lh = lane >> 5;
     const int n0 = blockIdx.x * 32, ks = blockIdx.y, m0 = blockIdx.z * 32;
     const int ksl = p.K / p.ksplit, kb = ks * ksl, G = ksl >> 6;
@@ -574,11 +576,19 @@ hipError_t mz_dec_gemm_launch(hipStream_t s, int epi, const MzDec& g) {
     if (epi == DEPI_LOGITS && (!g.sup || !g.amax || !g.ctr || g.M > 32 || g.N > 65536)) return hipErrorInvalidValue;
     if (epi != DEPI_PARTIAL && g.ksplit != 1) return hipErrorInvalidValue;
     const dim3 grid((g.N + 31) / 32, g.ksplit, (g.M + 31) / 32);
+    const int ksl = g.K / g.ksplit;
     switch (epi) {
-        case DEPI_PARTIAL: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_PARTIAL>, grid, dim3(256), 0, s, g); break;
-        case DEPI_GELU_F16: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_GELU_F16>, grid, dim3(256), 0, s, g); break;
-        case DEPI_QKV: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_QKV>, grid, dim3(256), 0, s, g); break;
-        case DEPI_F16: hipLaunchKernelGGL(dec_gemm_kernel<DEPI_F16>, grid, dim3(256), 0, s, g); break;
+        case DEPI_PARTIAL:
+            if (ksl <= 256) hipLaunchKernelGGL((dec_gemm_kernel<DEPI_PARTIAL, 256>), grid, dim3(256), 0, s, g);
+            else if (ksl <= 512) hipLaunchKernelGGL((dec_gemm_kernel<DEPI_PARTIAL, 512>), grid, dim3(256), 0, s, g);
+            else if (ksl <= 1024) hipLaunchKernelGGL((dec_gemm_kernel<DEPI_PARTIAL, 1024>), grid, dim3(256), 0, s, g);
+            else hipLaunchKernelGGL((dec_gemm_kernel<DEPI_PARTIAL, MZ_DEC_KSLICE>), grid, dim3(256), 0, s, g);
+            break;
+        case DEPI_GELU_F16:
+            hipLaunchKernelGGL((dec_gemm_kernel<DEPI_GELU_F16, MZ_DEC_KSLICE>), grid, dim3(256), 0, s, g);
+            break;
+        case DEPI_QKV: hipLaunchKernelGGL((dec_gemm_kernel<DEPI_QKV, MZ_DEC_KSLICE>), grid, dim3(256), 0, s, g); break;
+        case DEPI_F16: hipLaunchKernelGGL((dec_gemm_kernel<DEPI_F16, MZ_DEC_KSLICE>), grid, dim3(256), 0, s, g); break;
         case DEPI_LOGITS: {
             const int T = mz_lm_tiles_per_block(g.N);
             hipLaunchKernelGGL(dec_lmhead_kernel, dim3(mz_lm_blocks(g.N)), dim3(256), 0, s, g, T);
