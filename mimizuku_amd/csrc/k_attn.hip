@@ -112,7 +112,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
                 for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sc[r]), sc[r + 1]);
                 mx = fmaxf(mx, sc[15]);
-                mx = fmaxf(mx, __shfl_xor(mx, 32)) * cs - m[qs];  // block max over the running max
+                mx = pair32_max(mx) * cs - m[qs];  // block max over the running max
                 // first block: the max becomes this block's max; later: raised only past TAU (wave-uniform branch)
                 const bool first = kt == 0 && ss == 0;
                 if (__ballot(first || mx > TAU)) {
@@ -147,7 +147,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 
 #pragma unroll
     for (int qs = 0; qs < 2; qs++) {
-        const float lt = l[qs] + __shfl_xor(l[qs], 32);
+        const float lt = pair32_sum(l[qs]);
         const float inv = 1.f / lt;
         const int q = q0 + qs * 32 + lr;
         if (q >= MZ_TENC) continue;

@@ -66,6 +66,18 @@ __device__ __forceinline__ float wave_max(float v) {
                  fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)),
                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48))));
 }
+// lanes i and i ^ 32 combined, in both: v_permlane32_swap with both operands v returns (low half, high half) of v in
+// every lane, so no selection by lane is needed
+__device__ __forceinline__ float pair32_max(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+__device__ __forceinline__ float pair32_sum(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+}
 // (value, index) maximum over each aligned group of 8 lanes, ties to the lowest index, in every lane of the group
 __device__ __forceinline__ void group8_argmax(float& best, int& bi) {
     auto step = [&](float ov, int oi) {
