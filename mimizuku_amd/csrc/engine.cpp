@@ -670,13 +670,15 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
         g.ctr = e->ctr;
         return mz_dec_gemm_launch(s, epi, g);
     };
-    auto attn = [&](const float* q, int nq, const f16* qbias, const f16* k, const f16* v, long kv_b, int L,
-                    const int* aslot) {
+    auto attn = [&](const float* q, int nq, const f16* wq, const f16* qbias, const f16* k, const f16* v, long kv_b,
+                    int L, const int* aslot) {
         MzDecAttn a{};
         a.q = q;
         a.nq = nq;
         a.qstride = (long)b * D;
         a.qbias = qbias;
+        a.xin = wq ? e->h : nullptr;
+        a.wq = wq;
         a.k = k;
         a.v = v;
         a.kv_b = kv_b;
@@ -718,12 +720,12 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
             g.d = D;
             TRY(mz_dec_gemm_launch(s, DEPI_QKV, g), "dec qkv");
         }
-        TRY(attn(e->q, 1, nullptr, kc, vc, (long)nh * mt * HD, -1, nullptr), "self attention");
+        TRY(attn(e->q, 1, nullptr, nullptr, kc, vc, (long)nh * mt * HD, -1, nullptr), "self attention");
         TRY(gemm(DEPI_PARTIAL, e->datt, D, L.o, D, D, ks_dd, e->part, D), "dec out-proj");
         TRY(mz_dec_add_ln_launch(s, e->x, e->part, ks_dd, (long)b * D, L.o.b, L.lnx.w, L.lnx.b, e->h, b, D, EPS), "add+ln");
-        TRY(gemm(DEPI_PARTIAL, e->h, D, L.xq, D, D, ks_dd, e->part, D), "dec cross q");
-        TRY(attn(e->part, ks_dd, L.xq.b, e->xkvbuf + (size_t)(2 * i) * nh * blk, e->xkvbuf + (size_t)(2 * i + 1) * nh * blk,
-                 (long)nl * 2 * nh * blk, TENC, e->aslot + (size_t)i * nh),
+        // the cross-attention projects its own query from the layer-norm output
+        TRY(attn(nullptr, 0, L.xq.w, L.xq.b, e->xkvbuf + (size_t)(2 * i) * nh * blk,
+                 e->xkvbuf + (size_t)(2 * i + 1) * nh * blk, (long)nl * 2 * nh * blk, TENC, e->aslot + (size_t)i * nh),
             "cross attention");
         TRY(gemm(DEPI_PARTIAL, e->datt, D, L.xo, D, D, ks_dd, e->part, D), "dec cross out-proj");
         TRY(mz_dec_add_ln_launch(s, e->x, e->part, ks_dd, (long)b * D, L.xo.b, L.ln3.w, L.ln3.b, e->h, b, D, EPS), "add+ln");

@@ -408,9 +408,13 @@ __global__ void __launch_bounds__(256) dec_lmhead_kernel(const MzDec p, int T) {
 // AG groups of 8 lanes per workgroup, AU keys in flight per group: the cross-attention uses 32 x 8 (every (row, head)
 // workgroup of a 32-row batch resident at once, 64 KB in flight each), the self-attention over at most 448 cached
 // positions 64 x 4 (one pass over a 200-position cache).
+// The cross-attention's query projection runs in the same workgroup (wq set): its head's 64 rows of wq (read by the
+// 32 rows' workgroups of that head, so from L2 after the first) against the row's layer-norm output staged in LDS,
+// 8 lanes per weight row over whole 128-byte lines, with the first keys and values in flight behind them.
 template <int AG, int AU>
 __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
     __shared__ float qs[MZ_HD];
+    __shared__ __attribute__((aligned(16))) f16 xs[MZ_DEC_KSLICE];
     __shared__ float sc[MZ_TPAD];
     __shared__ float gm[AG], gl[AG];
     __shared__ float gacc[AG][MZ_HD + 1];
@@ -436,11 +440,50 @@ __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
             vv[u] = j < L ? __builtin_nontemporal_load((const f16x8*)(vb + (long)j * MZ_HD)) : f16x8{};
         }
     };
-    fetch(grp);
-    if (tid < MZ_HD) {
-        float q = a.qbias ? (float)a.qbias[head * MZ_HD + tid] : 0.f;
-        for (int s = 0; s < a.nq; s++) q += a.q[s * a.qstride + (long)b * a.d + head * MZ_HD + tid];
-        qs[tid] = q * (0.125f * 1.4426950408889634f);
+    constexpr float QS = 0.125f * 1.4426950408889634f;  // 1/8 and log2(e)
+    if (AG * 8 == 256 && a.wq) {
+        // q[i] = xin[b] . wq[head * 64 + i] + qbias: lane (r8, q8) of wave w takes rows 8 w + r8 and 32 + 8 w + r8,
+        // 16-byte chunks q8, q8 + 8, ... of each (nj per row); 8 lanes sum one row through DPP
+        const int w = tid >> 6, r8 = (tid >> 3) & 7, q8 = tid & 7, nj = a.d >> 6;
+        constexpr int NJ = MZ_DEC_KSLICE / 64;
+        const f16* wr = a.wq + (long)(head * MZ_HD + 8 * w + r8) * a.d + q8 * 8;
+        // in issue order: the row (one chunk per thread, d / 8 <= 160), the first 32 weight rows, the first keys and
+        // values; each wait below then covers only what it needs
+        const bool xl = tid < (a.d >> 3);
+        const f16x8 xv0 = xl ? *(const f16x8*)(a.xin + (long)b * a.d + tid * 8) : f16x8{};
+        f16x8 wv[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; j++) wv[j] = j < nj ? *(const f16x8*)(wr + j * 64) : f16x8{};
+        fetch(grp);
+        if (xl) *(f16x8*)&xs[tid * 8] = xv0;
+        __syncthreads();
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            float t = 0.f;
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                if (j < nj) {
+                    const f16x8 xv = *(const f16x8*)&xs[(q8 + 8 * j) * 8];
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2)
+                        t = __builtin_amdgcn_fdot2(f16x2{wv[j][e], wv[j][e + 1]}, f16x2{xv[e], xv[e + 1]}, t, false);
+                }
+            }
+            if (half == 0) {  // the second 32 rows, requested once the first ones are consumed
+#pragma unroll
+                for (int j = 0; j < NJ; j++) wv[j] = j < nj ? *(const f16x8*)(wr + 32L * a.d + j * 64) : f16x8{};
+            }
+            t = group8_sum(t);
+            const int i = 32 * half + 8 * w + r8;
+            if (q8 == 0) qs[i] = (t + (a.qbias ? (float)a.qbias[head * MZ_HD + i] : 0.f)) * QS;
+        }
+    } else {
+        fetch(grp);
+        if (tid < MZ_HD) {
+            float q = a.qbias ? (float)a.qbias[head * MZ_HD + tid] : 0.f;
+            for (int s = 0; s < a.nq; s++) q += a.q[s * a.qstride + (long)b * a.d + head * MZ_HD + tid];
+            qs[tid] = q * QS;
+        }
     }
     __syncthreads();
     float q8[8];
@@ -602,6 +645,8 @@ hipError_t mz_dec_gemm_launch(hipStream_t s, int epi, const MzDec& g) {
 hipError_t mz_dec_attn_launch(hipStream_t s, const MzDecAttn& a) {
     if (a.maxT <= 0 || a.B <= 0 || a.nh <= 0 || a.L > MZ_TPAD || (a.L <= 0 && a.maxT > MZ_TPAD)) return hipErrorInvalidValue;
     if (a.aslot && (!a.align || a.na <= 0 || (a.L > 0 && a.L != MZ_TENC))) return hipErrorInvalidValue;
+    // the fused query projection: cross-attention only, whole 64-half chunks per lane group, the row in LDS
+    if (a.wq && (a.L <= 0 || !a.xin || a.d % 64 != 0 || a.d > MZ_DEC_KSLICE)) return hipErrorInvalidValue;
     if (a.L > 0)
         hipLaunchKernelGGL((dec_attn_kernel<32, 8>), dim3(a.B * a.nh), dim3(32 * 8), 0, s, a);
     else

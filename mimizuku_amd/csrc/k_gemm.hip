@@ -7,10 +7,12 @@
 // other's products); each wave owns a (BM/2) x (BN/4) tile of 32x32x16 MFMA products. Both operands are
 // K-contiguous and go from global memory straight into LDS (buffer_load ... lds, 16 bytes per lane, no register
 // staging), double buffered: the loads of K tile k + 1 are in flight while tile k is multiplied, with one barrier per
-// K tile. In LDS a tile row is 64 halves (128 bytes) whose 16-byte chunks are XOR-swizzled by the row index, so the
-// ds_read_b128 operand fragments are conflict free; a direct load writes lane i's 16 bytes at base + 16 i, so each
-// lane fetches the global chunk that belongs at its swizzled position. Rows past the end of an operand (and the zero
-// padding of the implicit convolution) are read through the buffer descriptor's range check, which returns zeros.
+// K tile. In LDS a tile row is 64 halves (128 bytes) whose 16-byte chunks are XOR-swizzled by the row index (chunk c
+// of row r sits at position c ^ (r % 8) ^ (r / 8 % 2)): the 16 lanes that one ds_read_b128 cycle serves read 16
+// consecutive rows at one chunk, and these land in 16 distinct 16-byte bank groups of the 256-byte bank row; a
+// direct load writes lane i's 16 bytes at base + 16 i, so each lane fetches the global chunk that belongs at its
+// swizzled position. Rows past the end of an operand (and the zero padding of the implicit convolution) are read
+// through the buffer descriptor's range check, which returns zeros.
 // The activation tile is the MFMA A operand and the W tile the B operand, so lane l of a 32x32 product holds output
 // column l % 32 of eight rows: every store instruction writes two 32-column row segments. The transposed tiles of
 // the encoder's v are staged through LDS to be written as runs of token positions.
@@ -57,12 +59,14 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
     const int wm = wave >> 2, wn = wave & 3, lr = lane & 31, lh = lane >> 5;
     const int nk = p.K >> 6;
     // this lane's slot in a direct load: row lrow of an 8-row slice, 16-byte chunk lc of the row
+    // (slice r of a wave starts at a multiple of 8 rows whose bit 3 is r's bit 0)
     const int lrow = lane >> 3, lc = (lane & 7) ^ lrow;
+    static_assert((BM / NW) % 16 == 0 && (BN / NW) % 16 == 0, "a wave's slices must start on a 16-row boundary");
 
     const __amdgpu_buffer_rsrc_t rW = rsrc(p.W, (unsigned)p.N * p.K * 2);
     unsigned voW[WR];
 #pragma unroll
-    for (int r = 0; r < WR; r++) voW[r] = (unsigned)(bn * BN + wave * (BN / NW) + 8 * r + lrow) * p.K * 2 + lc * 16;
+    for (int r = 0; r < WR; r++) voW[r] = (unsigned)(bn * BN + wave * (BN / NW) + 8 * r + lrow) * p.K * 2 + (lc ^ (r & 1)) * 16;
     __amdgpu_buffer_rsrc_t rA;
     unsigned voA[AR];
     int srow[AR], stime[AR];  // conv: source row of tap 0 and its time index (-1 .. tin - 1), or a row past M
@@ -70,7 +74,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
         rA = rsrc(p.A, (unsigned)p.M * p.lda * 2);
 #pragma unroll
         for (int r = 0; r < AR; r++)
-            voA[r] = (unsigned)(bm * BM + wave * (BM / NW) + 8 * r + lrow) * p.lda * 2 + lc * 16;
+            voA[r] = (unsigned)(bm * BM + wave * (BM / NW) + 8 * r + lrow) * p.lda * 2 + (lc ^ (r & 1)) * 16;
     } else {
         const int clips = p.M / p.conv_tout;
         rA = rsrc(p.A, (unsigned)clips * p.conv_tin * p.conv_cin * 2);
@@ -91,9 +95,16 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
                                                          kt * 128, 0, 0);
         } else {
             // implicit im2col: column k = tap * cin + ci of a row reads source time stride * t + tap - 1
-            const int k0 = kt * 64 + lc * 8, tap = k0 / p.conv_cin, ci = k0 - tap * p.conv_cin;
+            int tap2[2], ci2[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int k0 = kt * 64 + (lc ^ h) * 8;
+                tap2[h] = k0 / p.conv_cin;
+                ci2[h] = k0 - tap2[h] * p.conv_cin;
+            }
 #pragma unroll
             for (int r = 0; r < AR; r++) {
+                const int tap = tap2[r & 1], ci = ci2[r & 1];
                 const int tt = stime[r] + tap;
                 const bool ok = tap < 3 && tt >= 0 && tt < p.conv_tin;
                 const unsigned vo = ok ? (unsigned)((srow[r] + tap) * p.conv_cin + ci) * 2 : OOB;
@@ -115,7 +126,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
     auto compute = [&](const f16* a, const f16* w) {
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
-            const int sw = (((2 * kk + lh) ^ (lr & 7)) << 3);
+            const int sw = (((2 * kk + lh) ^ (lr & 7) ^ ((lr >> 3) & 1)) << 3);
             f16x8 fa[TM], fw[TN];
 #pragma unroll
             for (int i = 0; i < TM; i++) fa[i] = *(const f16x8*)&a[(wm * WM + i * 32 + lr) * 64 + sw];

@@ -93,11 +93,14 @@ int mz_lm_blocks(int N);
 int mz_lm_tiles_per_block(int N);
 
 struct MzDecAttn {
-    // query: sum over nq slices of q[s * qstride + b * d + head * 64 + i] (+ qbias), scaled by 1/8
+    // query: sum over nq slices of q[s * qstride + b * d + head * 64 + i] (+ qbias), scaled by 1/8; or, when wq is
+    // set, the projection xin[b] . wq[head * 64 + i] (+ qbias) computed in the kernel (d <= MZ_DEC_KSLICE)
     const float* q;
     int nq;
     long qstride;
     const f16* qbias;
+    const f16* xin;  // [B][d]
+    const f16* wq;   // [d][d], row = output feature
     // keys and values of (b, head): rows of 64 halves at k + b * kv_b + head * kv_h (v likewise)
     const f16* k;
     const f16* v;
