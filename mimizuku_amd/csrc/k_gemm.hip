@@ -237,18 +237,19 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
         // offset is one lane base plus a wave-uniform row offset
         constexpr unsigned ES = EPI == EPI_RESID_F32 ? 4 : 2;
         const __amdgpu_buffer_rsrc_t rO = rsrc(p.out, (unsigned)(p.M * p.ldo) * ES);
-        const unsigned rs = (unsigned)p.ldo * ES;
+        // the row stride as an opaque scalar: each element's offset is then one vector add of a scalar row offset
+        const unsigned rs = __builtin_amdgcn_readfirstlane((unsigned)p.ldo * ES);
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             const int n = n0 + j * 32 + lr;
             if (n >= p.N) continue;
             const float bv = p.bias ? (float)p.bias[n] : 0.f;
-            const unsigned vb = (unsigned)((m0 + 4 * lh) * p.ldo + n) * ES;
+            // rows m0 + 4 lh + i * 32 + 8 (r / 4) + r % 4 in order: one row further, five after every fourth
+            unsigned off = (unsigned)((m0 + 4 * lh) * p.ldo + n) * ES;
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const unsigned off = vb + (unsigned)(i * 32 + 8 * (r >> 2) + (r & 3)) * rs;
+                for (int r = 0; r < 16; r++, off += (r & 3) == 0 ? 5 * rs : rs) {
                     const float v = acc[i][j][r] + bv;
                     if (EPI == EPI_F16) {
                         __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (f16)v), rO, off, 0, 0);

@@ -116,17 +116,18 @@ __device__ __forceinline__ void wave_argmax(float& best, int& bi) {
 }
 
 // Exact (erf) GELU, as nn.GELU(): 0.5 v (1 + erf(v / sqrt 2)), with erf from Abramowitz & Stegun 7.1.26 (Hastings'
-// rational approximation, |error| <= 1.5e-7 on erf): 1 + erf(u) = 2 - q for u >= 0 and q for u < 0, where
-// q = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-u^2), t = 1 / (1 + p |u|); the negative side is evaluated without
-// cancellation. Far cheaper than the device library's erff in the fc1 epilogues; within one fp16 ulp of the exact
-// GELU over the whole range (checked against scipy's erf in the tests).
+// rational approximation, |error| <= 1.5e-7 on erf). With u = |v| / sqrt 2, t = 1 / (1 + p u) and
+// h = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-u^2) / 2 = (1 - erf(u)) / 2, GELU(v) = v (1 - h) for v >= 0 and
+// v h for v < 0, so the negative side has no cancellation (the halving is folded into the coefficients, p / sqrt 2
+// into one constant). Against the exact GELU rounded to fp16: correctly rounded except in the tail where 1 - erf(u) is
+// below ~1e-4, at most 1.46 fp16 ulp (v in [-4.3, -3.6]); the reference's own fp32 formula reaches 1.7 ulp there from
+// the cancellation in 1 + erf(u).
 __device__ __forceinline__ float gelu_erf(float v) {
-    const float u = fabsf(v) * 0.70710678118654752f;
-    const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, u, 1.f));
-    const float poly =
-        t * fmaf(t, fmaf(t, fmaf(t, fmaf(t, 1.061405429f, -1.453152027f), 1.421413741f), -0.284496736f), 0.254829592f);
-    const float q = poly * __builtin_amdgcn_exp2f(-u * u * 1.4426950408889634f);
-    return 0.5f * v * (v >= 0.f ? 2.f - q : q);
+    const float t = __builtin_amdgcn_rcpf(fmaf(fabsf(v), 0.3275911f * 0.70710678118654752f, 1.f));
+    const float hp = t * fmaf(t, fmaf(t, fmaf(t, fmaf(t, 0.5307027145f, -0.7265760135f), 0.7107068705f), -0.142248368f),
+                              0.127414796f);
+    const float h = hp * __builtin_amdgcn_exp2f(v * (v * (-0.5f * 1.4426950408889634f)));
+    return v * (v >= 0.f ? 1.f - h : h);
 }
 
 // A workgroup barrier for LDS traffic only: waits for this wave's LDS operations (lgkmcnt(0)) but not for its
