@@ -456,7 +456,7 @@ __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
         for (int j = 0; j < NJ; j++) wv[j] = j < nj ? *(const f16x8*)(wr + j * 64) : f16x8{};
         fetch(grp);
         if (xl) *(f16x8*)&xs[tid * 8] = xv0;
-        __syncthreads();
+        lds_barrier();  // the row in LDS; the weight rows, keys and values stay in flight
 #pragma unroll
         for (int half = 0; half < 2; half++) {
             float t = 0.f;
