@@ -11,10 +11,11 @@
 // 16-byte LDS loads.
 //
 // On this part the vector ALU and the matrix cores of a SIMD do not overlap (an MFMA and the vector instructions
-// around it take the sum of their times), so every vector instruction per score counts: the running max is raised
-// only when a block's scores exceed it by more than 2^8 (p = exp2(s - m) <= 256 is exact enough in fp16 and keeps
-// the rescale of O rare), the row sums add the fp16 probabilities two per dot2 instruction, and the key mask of the
-// padded last tile is applied in that tile only.
+// around it take the sum of their times), so every vector instruction per score counts: the running max is set by
+// the first block and later blocks compute no max at all; a block is recomputed against its own max (and O
+// rescaled) only when the sum of its probabilities reaches 2^12, i.e. some p = exp2(s - m) could leave the range
+// where fp16 holds it exactly enough; the probabilities are rounded two per packed conversion and summed two per
+// dot2 instruction, and the key mask of the padded last tile is applied in that tile only.
 #include <type_traits>
 
 #include "mz_common.h"
@@ -27,6 +28,31 @@ constexpr int QB = 256; // queries per block
 constexpr int NT = MZ_TPAD / 64;  // key tiles (the last one holds keys 1472..1535, valid < 1500)
 
 __device__ __forceinline__ int swap23(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float block_max(const f32x16& sc) {
+    float mx = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
+#pragma unroll
+    for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sc[r]), sc[r + 1]);
+    return fmaxf(mx, sc[15]);
+}
+
+// p = exp2(s * log2(e) / 8 - m) rounded to fp16 two at a time (one packed conversion per pair, each pair one dword
+// of the P.V operand), and the sum of the rounded values (the ones that weight V) through dot2 in fp32
+__device__ __forceinline__ float probs(const f32x16& sc, float m, unsigned (&pw)[2][4]) {
+    constexpr float cs = 0.125f * 1.4426950408889634f;
+    float lb = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+        const f32x2 e = {__builtin_amdgcn_exp2f(fmaf(sc[r], cs, -m)), __builtin_amdgcn_exp2f(fmaf(sc[r + 1], cs, -m))};
+        const f16x2 h = __builtin_convertvector(e, f16x2);
+        lb = __builtin_amdgcn_fdot2(h, f16x2{1, 1}, lb, false);
+        pw[r >> 3][(r & 7) >> 1] = __builtin_bit_cast(unsigned, h);
+    }
+    return lb;
+}
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) enc_attn_kernel(const f16* __restrict__ qkvh, f16* __restrict__ out, int nh, int G) {
     __shared__ __attribute__((aligned(16))) f16 sK[2][64 * KP];
@@ -71,8 +97,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         *(f16x8*)&sV[buf][kr1 * KP + cc] = pv1;
     };
 
-    constexpr float TAU = 8.f;  // log2 of the largest unnormalised probability before O is rescaled
-    float m[2] = {0.f, 0.f};    // running max of the scaled scores (per query column); set by the first block
+    float m[2] = {0.f, 0.f};  // running max of the scaled scores (per query column); set by the first block
     float l[2] = {0.f, 0.f};
     f32x16 o[2][2];
 #pragma unroll
@@ -108,15 +133,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                         if (key >= MZ_TENC) sc[r] = -INFINITY;
                     }
                 }
-                float mx = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
-#pragma unroll
-                for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sc[r]), sc[r + 1]);
-                mx = fmaxf(mx, sc[15]);
-                mx = pair32_max(mx) * cs - m[qs];  // block max over the running max
-                // first block: the max becomes this block's max; later: raised only past TAU (wave-uniform branch)
+                // the first block sets the running max (l and o are still zero)
                 const bool first = kt == 0 && ss == 0;
-                if (__ballot(first || mx > TAU)) {
-                    const float dm = (first || mx > TAU) ? mx : 0.f;
+                if (first) m[qs] = pair32_max(block_max(sc)) * cs;
+                unsigned pw[2][4];
+                float lb = probs(sc, m[qs], pw);
+                // later blocks raise it only when their probabilities get large: a block sum of 2^12 or more (some
+                // score more than 8 above the running max, or an fp16 overflow) recomputes the block against its
+                // own max; below that every probability is < 2^12, exact enough in fp16 (wave-uniform branch)
+                if (!first && __ballot(!(lb < 4096.f))) {
+                    const float mx = pair32_max(block_max(sc)) * cs - m[qs];
+                    const float dm = mx > 0.f ? mx : 0.f;
                     const float corr = __builtin_amdgcn_exp2f(-dm);
                     m[qs] += dm;
                     l[qs] *= corr;
@@ -124,19 +151,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                     for (int t = 0; t < 2; t++)
 #pragma unroll
                         for (int r = 0; r < 16; r++) o[qs][t][r] *= corr;
+                    lb = probs(sc, m[qs], pw);
                 }
-                f16x8 pf[2];
-#pragma unroll
-                for (int r = 0; r < 16; r++) pf[r >> 3][r & 7] = (f16)__builtin_amdgcn_exp2f(fmaf(sc[r], cs, -m[qs]));
-                // row sum of the fp16 probabilities (the ones that weight V), two per dot2 with fp32 accumulation
-#pragma unroll
-                for (int r = 0; r < 16; r += 2)
-                    l[qs] = __builtin_amdgcn_fdot2(f16x2{pf[r >> 3][r & 7], pf[r >> 3][(r & 7) + 1]}, f16x2{1, 1}, l[qs],
-                                                   false);
+                l[qs] += lb;
 #pragma unroll
                 for (int t = 0; t < 2; t++)
 #pragma unroll
-                    for (int c = 0; c < 2; c++) o[qs][t] = mfma32(vf[t][c], pf[c], o[qs][t]);
+                    for (int c = 0; c < 2; c++)
+                        o[qs][t] = mfma32(vf[t][c], __builtin_bit_cast(f16x8, u32x4{pw[c][0], pw[c][1], pw[c][2], pw[c][3]}),
+                                          o[qs][t]);
             }
         }
         if (!LAST) lstore(buf ^ 1);
