@@ -80,15 +80,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int c = 0; c < 4; c++) qf[s][c] = ld8(Q + (long)(q0 + s * 32 + lr) * MZ_HD + 16 * c + 8 * lh);
 
-    // this thread's two K chunks and two V^T chunks of a tile
+    // this thread's two K chunks and two V^T chunks of a tile: buffer loads with a fixed per-lane offset and the tile
+    // step in the scalar offset (no address arithmetic per tile; every offset lies within the padded head block)
     const int c0 = tid, c1 = tid + 256;
     const int kr0 = c0 >> 3, kr1 = c1 >> 3, cc = (tid & 7) * 8;
+    const __amdgpu_buffer_rsrc_t rK = rsrc(K, MZ_TPAD * MZ_HD * 2), rV = rsrc(Vt, MZ_HD * MZ_TPAD * 2);
+    const unsigned ok0 = (kr0 * MZ_HD + cc) * 2, ok1 = (kr1 * MZ_HD + cc) * 2;
+    const unsigned ov0 = (kr0 * MZ_TPAD + cc) * 2, ov1 = (kr1 * MZ_TPAD + cc) * 2;
     f16x8 pk0, pk1, pv0, pv1;
     auto gload = [&](int kt) {
-        pk0 = ld8(K + (long)(kt * 64 + kr0) * MZ_HD + cc);
-        pk1 = ld8(K + (long)(kt * 64 + kr1) * MZ_HD + cc);
-        pv0 = ld8(Vt + (long)kr0 * MZ_TPAD + kt * 64 + cc);
-        pv1 = ld8(Vt + (long)kr1 * MZ_TPAD + kt * 64 + cc);
+        const int sk = kt * 64 * MZ_HD * 2, sv = kt * 64 * 2;
+        pk0 = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rK, ok0, sk, 0));
+        pk1 = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rK, ok1, sk, 0));
+        pv0 = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rV, ov0, sv, 0));
+        pv1 = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rV, ov1, sv, 0));
     };
     auto lstore = [&](int buf) {
         *(f16x8*)&sK[buf][swap23(kr0) * KP + cc] = pk0;

@@ -126,13 +126,6 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int MZ_NT = 2;  // cache-policy bit of a buffer load: nontemporal (weights are streamed once per step)
 
-// Workgroup barrier that waits for this wave's LDS operations only, not for its loads in flight (a __syncthreads
-// would also wait for every outstanding global load); the memory clobber keeps the compiler from moving LDS
-// accesses across it.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigned bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
 // One workgroup per (32 output columns, K slice, 32 rows): both operands of its K slice (<= MZ_DEC_KSLICE) go from
 // memory straight into LDS with every load issued at once (buffer_load ... lds, 16 bytes per lane), in 1 KB blocks of
 // 8 rows x 64 halves: lane i of a load writes block bytes 16 i, so one load reads 8 whole 128-byte rows (full cache

@@ -26,10 +26,6 @@ typedef __attribute__((address_space(3))) void lds_void;
 #define LDSP(p) ((lds_void*)(p))
 constexpr unsigned OOB = 0x80000000u;  // a buffer offset past every operand: the load returns zeros
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigned bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
 // Workgroup i runs on XCD i % 8, and each XCD has its own L2. XCD x owns a band of rows = ceil(nbm / 8) block rows
 // and visits its tiles with the block row fastest: the band's activation panels stay in its L2 while each weight
 // panel is read once per XCD and shared by the band's tiles that run at the same time. The grid is 8 * rows * nbn.

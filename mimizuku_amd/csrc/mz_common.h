@@ -137,6 +137,12 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_barrier" ::: "memory");
 }
 
+// A raw buffer resource over `bytes` bytes at base (stride 0, dword data format): loads at offsets past the end
+// return zeros and stores there are dropped; the range check covers the per-lane offset, not the scalar one.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
 __device__ __forceinline__ f16x8 ld8(const f16* p) { return *(const f16x8*)p; }
 __device__ __forceinline__ void st4(f16* p, float a, float b, float c, float d) {
     f16x4 v = {(f16)a, (f16)b, (f16)c, (f16)d};
