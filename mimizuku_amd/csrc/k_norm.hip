@@ -9,9 +9,17 @@ namespace {
 constexpr int MAXC = 8;  // float4 chunks per lane: dim <= 2048
 
 // LayerNorm of one row held as v[i] = x[4 (lane + 64 i) .. + 4] (chunks past dim / 4 hold zeros and are not
-// stored), written to y as fp16. Two-pass statistics (mean, then the centred second moment) as the reference.
+// stored), written to y as fp16. Two-pass statistics (mean, then the centred second moment) as the reference. The
+// gamma / beta loads go out before the reductions.
 __device__ __forceinline__ void ln_store(const float4 (&v)[MAXC], int nc, int lane, const f16* __restrict__ w,
                                          const f16* __restrict__ b, f16* __restrict__ y, int dim, float eps) {
+    f16x4 wv[MAXC], bv[MAXC];
+#pragma unroll
+    for (int i = 0; i < MAXC; i++)
+        if (lane + 64 * i < nc) {
+            wv[i] = *(const f16x4*)(w + (lane + 64 * i) * 4);
+            bv[i] = *(const f16x4*)(b + (lane + 64 * i) * 4);
+        }
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < MAXC; i++)
@@ -29,10 +37,11 @@ __device__ __forceinline__ void ln_store(const float4 (&v)[MAXC], int nc, int la
     for (int i = 0; i < MAXC; i++)
         if (lane + 64 * i < nc) {
             const int idx = (lane + 64 * i) * 4;
-            const f16x4 wv = *(const f16x4*)(w + idx), bv = *(const f16x4*)(b + idx);
-            st4(y + idx, (v[i].x - mean) * rstd * (float)wv[0] + (float)bv[0],
-                (v[i].y - mean) * rstd * (float)wv[1] + (float)bv[1], (v[i].z - mean) * rstd * (float)wv[2] + (float)bv[2],
-                (v[i].w - mean) * rstd * (float)wv[3] + (float)bv[3]);
+            const f16x4 o = {(f16)((v[i].x - mean) * rstd * (float)wv[i][0] + (float)bv[i][0]),
+                             (f16)((v[i].y - mean) * rstd * (float)wv[i][1] + (float)bv[i][1]),
+                             (f16)((v[i].z - mean) * rstd * (float)wv[i][2] + (float)bv[i][2]),
+                             (f16)((v[i].w - mean) * rstd * (float)wv[i][3] + (float)bv[i][3])};
+            __builtin_nontemporal_store(o, (f16x4*)(y + idx));
         }
 }
 
@@ -61,11 +70,13 @@ __global__ void __launch_bounds__(256) add_ln_kernel(float* __restrict__ x, cons
     const f16* dr = d + (long)row * dim;
     float4 v[MAXC];
     f16x4 dv[MAXC];
+    // the residual and the delta are streamed once: nontemporal loads and stores
 #pragma unroll
     for (int i = 0; i < MAXC; i++) {
         const bool on = lane + 64 * i < nc;
-        v[i] = on ? *(const float4*)(xr + (lane + 64 * i) * 4) : float4{};
-        dv[i] = on ? *(const f16x4*)(dr + (lane + 64 * i) * 4) : f16x4{};
+        const f32x4 t = on ? __builtin_nontemporal_load((const f32x4*)(xr + (lane + 64 * i) * 4)) : f32x4{};
+        v[i] = float4{t[0], t[1], t[2], t[3]};
+        dv[i] = on ? __builtin_nontemporal_load((const f16x4*)(dr + (lane + 64 * i) * 4)) : f16x4{};
     }
 #pragma unroll
     for (int i = 0; i < MAXC; i++)
@@ -74,7 +85,7 @@ __global__ void __launch_bounds__(256) add_ln_kernel(float* __restrict__ x, cons
             v[i].y += (float)dv[i][1];
             v[i].z += (float)dv[i][2];
             v[i].w += (float)dv[i][3];
-            *(float4*)(xr + (lane + 64 * i) * 4) = v[i];
+            __builtin_nontemporal_store(f32x4{v[i].x, v[i].y, v[i].z, v[i].w}, (f32x4*)(xr + (lane + 64 * i) * 4));
         }
     ln_store(v, nc, lane, w, b, y + (long)row * dim, dim, eps);
 }
