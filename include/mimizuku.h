@@ -91,8 +91,8 @@ typedef struct {
     uint64_t pos; /* MZ_EPI_GELU_POS: f16 [1500][n] */
     /* MZ_EPI_HEADS: column n -> block n / 64, row m -> clip m / 1500, time m % 1500; the block's tile is at
      * heads + ((slot0 + clip) * blocks_per_clip + block) * 1536 * 64 halves. kind 3: blocks [q|k|v][head] (encoder
-     * self-attention; the v tiles stored transposed [64][1536]), kind 2: [layer][k|v][head] (cross-attention; every
-     * tile row-major [1536][64]). */
+     * self-attention; the q tiles stored multiplied by log2(e) / 8, the v tiles transposed [64][1536]), kind 2:
+     * [layer][k|v][head] (cross-attention; every tile row-major [1536][64]). */
     uint64_t heads;
     int blocks_per_clip, nh, kind, slot0;
     /* implicit conv1d (kernel 3, padding 1): A[clip * conv_tout + t][tap * cin + ci] =
@@ -108,7 +108,8 @@ int mz_layernorm(mz_ctx* c, uint64_t x, long ldx, uint64_t w, uint64_t b, uint64
 int mz_add_layernorm(mz_ctx* c, uint64_t x, uint64_t d, uint64_t w, uint64_t b, uint64_t y, int rows, int dim,
                      float eps);
 /* Encoder self-attention (enc_flash, whisper.cu:168-299): qkvh [clips][3][nh] tiles of 1536 x 64 halves
- * (q, k as [t][64]; v transposed [64][t]; t >= 1500 zero) -> out f16 [clips * 1500][nh * 64]; scale 1/8. */
+ * (q, k as [t][64]; v transposed [64][t]; t >= 1500 zero) -> out f16 [clips * 1500][nh * 64]; scale 1/8. The q tiles
+ * hold q multiplied by log2(e) / 8, as the QKV product (mz_linear, EPI_HEADS, kind 3) writes them. */
 int mz_enc_attention(mz_ctx* c, uint64_t qkvh, uint64_t out, int clips, int nh);
 /* log-mel f32 [clips][n_mels][3000] -> f16 [clips][3000][n_mels] (the conv stem's source layout). */
 int mz_mel_transpose(mz_ctx* c, uint64_t mel, uint64_t melT, int clips, int n_mels);

@@ -39,14 +39,14 @@ __device__ __forceinline__ float block_max(const f32x16& sc) {
     return fmaxf(mx, sc[15]);
 }
 
-// p = exp2(s * log2(e) / 8 - m) rounded to fp16 two at a time (one packed conversion per pair, each pair one dword
-// of the P.V operand), and the sum of the rounded values (the ones that weight V) through dot2 in fp32
-__device__ __forceinline__ float probs(const f32x16& sc, float m, unsigned (&pw)[2][4]) {
-    constexpr float cs = 0.125f * 1.4426950408889634f;
+// p = exp2(sc) (the scores already in log2 units and relative to the running max) rounded to fp16 two at a time (one
+// packed conversion per pair, each pair one dword of the P.V operand), and the sum of the rounded values (the ones
+// that weight V) through dot2 in fp32
+__device__ __forceinline__ float probs(const f32x16& sc, unsigned (&pw)[2][4]) {
     float lb = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; r += 2) {
-        const f32x2 e = {__builtin_amdgcn_exp2f(fmaf(sc[r], cs, -m)), __builtin_amdgcn_exp2f(fmaf(sc[r + 1], cs, -m))};
+        const f32x2 e = {__builtin_amdgcn_exp2f(sc[r]), __builtin_amdgcn_exp2f(sc[r + 1])};
         const f16x2 h = __builtin_convertvector(e, f16x2);
         lb = __builtin_amdgcn_fdot2(h, f16x2{1, 1}, lb, false);
         pw[r >> 3][(r & 7) >> 1] = __builtin_bit_cast(unsigned, h);
@@ -71,8 +71,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     const f16* Vt = Q + 2L * nh * blk;
     const int d = nh * MZ_HD;
 
-    // query fragments (B operand of S^T): query row, dims 16c + 8 lh .. + 8
-    const float cs = 0.125f * 1.4426950408889634f;  // scale * log2(e)
+    // query fragments (B operand of S^T): query row, dims 16c + 8 lh .. + 8; the QKV product stores q multiplied by
+    // log2(e) / 8, so the products are the scores in log2 units
     const int q0 = qb * QB + wave * 64;
     f16x8 qf[2][4];
 #pragma unroll
@@ -102,7 +102,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         *(f16x8*)&sV[buf][kr1 * KP + cc] = pv1;
     };
 
-    float m[2] = {0.f, 0.f};  // running max of the scaled scores (per query column); set by the first block
+    // running max of the scores (per query column), set by the first block, kept as -m in all 16 elements of the C
+    // input of each block's first product: the scores come out of the matrix core relative to it
+    float m[2] = {0.f, 0.f};
+    f32x16 cm[2] = {f32x16{}, f32x16{}};
     float l[2] = {0.f, 0.f};
     f32x16 o[2][2];
 #pragma unroll
@@ -128,9 +131,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                     vf[t][c] = *(const f16x8*)&sV[buf][(32 * t + lr) * KP + 32 * ss + 16 * c + 8 * lh];
 #pragma unroll
             for (int qs = 0; qs < 2; qs++) {
-                f32x16 sc = {};
+                f32x16 sc = mfma32(kf[0], qf[qs][0], cm[qs]);
 #pragma unroll
-                for (int c = 0; c < 4; c++) sc = mfma32(kf[c], qf[qs][c], sc);
+                for (int c = 1; c < 4; c++) sc = mfma32(kf[c], qf[qs][c], sc);
                 if (LAST) {
 #pragma unroll
                     for (int r = 0; r < 16; r++) {
@@ -140,23 +143,35 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                 }
                 // the first block sets the running max (l and o are still zero)
                 const bool first = kt == 0 && ss == 0;
-                if (first) m[qs] = pair32_max(block_max(sc)) * cs;
+                if (first) {
+                    m[qs] = pair32_max(block_max(sc));
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        sc[r] -= m[qs];
+                        cm[qs][r] = -m[qs];
+                    }
+                }
                 unsigned pw[2][4];
-                float lb = probs(sc, m[qs], pw);
+                float lb = probs(sc, pw);
                 // later blocks raise it only when their probabilities get large: a block sum of 2^12 or more (some
                 // score more than 8 above the running max, or an fp16 overflow) recomputes the block against its
                 // own max; below that every probability is < 2^12, exact enough in fp16 (wave-uniform branch)
                 if (!first && __ballot(!(lb < 4096.f))) {
-                    const float mx = pair32_max(block_max(sc)) * cs - m[qs];
+                    const float mx = pair32_max(block_max(sc));
                     const float dm = mx > 0.f ? mx : 0.f;
                     const float corr = __builtin_amdgcn_exp2f(-dm);
                     m[qs] += dm;
                     l[qs] *= corr;
 #pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        sc[r] -= dm;
+                        cm[qs][r] = -m[qs];
+                    }
+#pragma unroll
                     for (int t = 0; t < 2; t++)
 #pragma unroll
                         for (int r = 0; r < 16; r++) o[qs][t][r] *= corr;
-                    lb = probs(sc, m[qs], pw);
+                    lb = probs(sc, pw);
                 }
                 l[qs] += lb;
 #pragma unroll

@@ -207,6 +207,8 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
         const __amdgpu_buffer_rsrc_t rH =
             rsrc(p.heads + (p.slot0 + g0) * clip, ncl > 0 ? (unsigned)(ncl * clip * 2) : 0u);
         const int blk = n0 >> 6, c0 = (n0 & 63) + lr;
+        // the encoder's q tiles are stored multiplied by log2(e) / 8, the attention's exponent scale
+        const float qsc = (p.kind == 3 && blk < p.nh) ? 0.125f * 1.4426950408889634f : 1.f;
 #pragma unroll
         for (int i = 0; i < TM; i++) {
             const int mb = m0 + i * 32 + 4 * lh, gb = mb / MZ_TENC, tb = mb - gb * MZ_TENC;
@@ -216,13 +218,13 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 const int n = n0 + j * 32 + lr;
-                const float bv = p.bias ? (float)p.bias[min(n, p.N - 1)] : 0.f;
+                const float bv = (p.bias ? (float)p.bias[min(n, p.N - 1)] : 0.f) * qsc;
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int dr = 8 * (r >> 2) + (r & 3);
                     const unsigned e = cb + j * 32 + dr * MZ_HD + (tb + dr >= MZ_TENC ? wrap : 0u);
-                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (f16)(acc[i][j][r] + bv)), rH,
-                                                          e * 2, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (f16)fmaf(acc[i][j][r], qsc, bv)),
+                                                          rH, e * 2, 0, 0);
                 }
             }
         }

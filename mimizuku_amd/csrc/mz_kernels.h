@@ -31,8 +31,9 @@ struct MzGemm {
     const f16* pos;
     // EPI_HEADS: column n belongs to 64-wide block blk = n / 64 and row m = g * 1500 + t to clip g; the block's
     // 1536 x 64 tile lives at heads + ((slot0 + g) * blocks_per_clip + blk) * 1536 * 64. kind 3: blocks ordered
-    // [q|k|v][head] (encoder self-attention; v stored transposed [64][1536] for the P.V matrix product), kind 2:
-    // [layer][k|v][head] (decoder cross-attention; every tile row-major [1536][64]).
+    // [q|k|v][head] (encoder self-attention; q stored multiplied by log2(e) / 8, the attention's exponent scale, and
+    // v transposed [64][1536] for the P.V matrix product), kind 2: [layer][k|v][head] (decoder cross-attention;
+    // every tile row-major [1536][64]).
     f16* heads;
     int blocks_per_clip, nh, kind, slot0;
 };

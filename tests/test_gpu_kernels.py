@@ -63,9 +63,20 @@ def pack_qkvh(q, k, v):
     return out
 
 
-def run_attention(ctx, q, k, v):
-    G, nh = q.shape[:2]
-    dq = ctx.upload_new(pack_qkvh(q, k, v))
+QSCALE = 0.125 * np.log2(np.e)  # the QKV product stores q multiplied by the attention's exponent scale
+
+
+def prescaled(q):
+    """(q as the QKV product stores it: fp16(q x log2(e) / 8), the query that stored value stands for) - the kernel's
+    input and the reference's."""
+    qs = (q.astype(np.float64) * QSCALE).astype(np.float16)
+    return qs, qs.astype(np.float64) / QSCALE
+
+
+def run_attention(ctx, qs, k, v):
+    """qs: prescaled(q)[0]"""
+    G, nh = qs.shape[:2]
+    dq = ctx.upload_new(pack_qkvh(qs, k, v))
     do = ctx.alloc(G * 1500 * nh * 64 * 2)
     L.check(L.lib().mz_enc_attention(ctx.h, dq, do, G, nh))
     out = ctx.download(do, (G, 1500, nh, 64), np.float16)
@@ -96,7 +107,8 @@ def attention_bar(q, k, v, ref):
 def test_enc_attention_small(ctx):
     rng = np.random.default_rng(10)
     q, k, v = (f16(rng, (1, 2, 1500, 64)) for _ in range(3))
-    out = run_attention(ctx, q, k, v)
+    qs, q = prescaled(q)
+    out = run_attention(ctx, qs, k, v)
     ref = attention64(q, k, v)
     assert rel_err(out, ref) < attention_bar(q, k, v, ref)
     # a transposed V (a plausible layout mistake) is far outside the bar
@@ -108,7 +120,8 @@ def test_enc_attention_peaked_scores(ctx):
     rng = np.random.default_rng(11)
     q, k = f16(rng, (1, 1, 1500, 64), 4.0), f16(rng, (1, 1, 1500, 64), 4.0)
     v = f16(rng, (1, 1, 1500, 64))
-    out = run_attention(ctx, q, k, v)
+    qs, q = prescaled(q)
+    out = run_attention(ctx, qs, k, v)
     ref = attention64(q, k, v)
     assert rel_err(out, ref) < attention_bar(q, k, v, ref)
 
@@ -119,7 +132,8 @@ def test_enc_attention_large_v3_shape(ctx):
     rng = np.random.default_rng(12)
     shape = (8, 20, 1500, 64)
     q, k, v = (f16(rng, shape) for _ in range(3))
-    out = run_attention(ctx, q, k, v)
+    qs, q = prescaled(q)
+    out = run_attention(ctx, qs, k, v)
     rows = np.r_[np.arange(0, 1500, 37), 1496, 1497, 1498, 1499]
     ref = attention64(q[:, :, rows], k, v)
     assert rel_err(out[:, :, rows], ref) < attention_bar(q[:, :, rows], k, v, ref)
@@ -180,8 +194,9 @@ def test_gemm_epilogues(ctx):
 
 @pytest.mark.parametrize("kind", [3, 2])
 def test_gemm_head_scatter(ctx, kind):
-    """kind 3: [q|k|v][head] tiles of the encoder self-attention (v tiles transposed); kind 2: [layer][k|v][head] of
-    the cross k/v (all tiles row-major); both into clip slots (slot0 offset)."""
+    """kind 3: [q|k|v][head] tiles of the encoder self-attention (v tiles transposed, q tiles multiplied by
+    log2(e) / 8); kind 2: [layer][k|v][head] of the cross k/v (all tiles row-major); both into clip slots (slot0
+    offset)."""
     rng = np.random.default_rng(kind)
     nh, clips, slot0 = 2, 2, 1
     groups = 3 if kind == 3 else 2 * 2  # kind 2: two decoder layers
@@ -195,6 +210,8 @@ def test_gemm_head_scatter(ctx, kind):
                                                  heads=dh, blocks_per_clip=bpc, nh=nh, kind=kind, slot0=slot0)))
     got = ctx.download(dh, (nslots, bpc, TPAD * 64), np.float16)
     ref = (x.astype(np.float64) @ w.astype(np.float64).T + b).reshape(clips, 1500, bpc, 64)
+    if kind == 3:
+        ref[:, :, :nh] *= QSCALE
     assert not got[:slot0].any(), "a slot before slot0 was written"
     assert not got[slot0 + clips:].any(), "a slot after the last clip was written"
     for c in range(clips):
