@@ -7,7 +7,7 @@
 // other's products); each wave owns a (BM/2) x (BN/4) tile of 32x32x16 MFMA products. Both operands are
 // K-contiguous and go from global memory straight into LDS (buffer_load ... lds, 16 bytes per lane, no register
 // staging), double buffered: the loads of K tile k + 1 are in flight while tile k is multiplied, with one barrier per
-// K tile. In LDS a tile row is 64 halves (128 bytes) whose 16-byte chunks are XOR-swizzled by the row index (chunk c
+// K tile; the operand fragments are software pipelined a 16-wide K step ahead of the products. In LDS a tile row is 64 halves (128 bytes) whose 16-byte chunks are XOR-swizzled by the row index (chunk c
 // of row r sits at position c ^ (r % 8) ^ (r / 8 % 2)): the 16 lanes that one ds_read_b128 cycle serves read 16
 // consecutive rows at one chunk, and these land in 16 distinct 16-byte bank groups of the 256-byte bank row; a
 // direct load writes lane i's 16 bytes at base + 16 i, so each lane fetches the global chunk that belongs at its
@@ -119,20 +119,54 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = f32x16{};
-    auto compute = [&](const f16* a, const f16* w) {
+    // Fragments of K step kk (16 wide) of a tile: TM A and TN W fragments. They are double buffered across steps:
+    // step kk + 1's reads go out while step kk's products issue, one read between two products (explicit scheduling
+    // groups; the hardware interleaves the two waves of a SIMD on top). The last step's products are split around
+    // the tile's wait and barrier, so that the next tile's first fragments are read under the second half.
+    f16x8 fa0[TM], fw0[TN], fa1[TM], fw1[TN];
+    auto frags = [&](const f16* a, const f16* w, int kk, f16x8(&fa)[TM], f16x8(&fw)[TN]) {
+        const int sw = (((2 * kk + lh) ^ (lr & 7) ^ ((lr >> 3) & 1)) << 3);
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            const int sw = (((2 * kk + lh) ^ (lr & 7) ^ ((lr >> 3) & 1)) << 3);
-            f16x8 fa[TM], fw[TN];
+        for (int i = 0; i < TM; i++) fa[i] = *(const f16x8*)&a[(wm * WM + i * 32 + lr) * 64 + sw];
 #pragma unroll
-            for (int i = 0; i < TM; i++) fa[i] = *(const f16x8*)&a[(wm * WM + i * 32 + lr) * 64 + sw];
+        for (int j = 0; j < TN; j++) fw[j] = *(const f16x8*)&w[(wn * WN + j * 32 + lr) * 64 + sw];
+    };
+    auto mma = [&](const f16x8(&fa)[TM], const f16x8(&fw)[TN], int i0, int i1) {
 #pragma unroll
-            for (int j = 0; j < TN; j++) fw[j] = *(const f16x8*)&w[(wn * WN + j * 32 + lr) * 64 + sw];
+        for (int i = i0; i < i1; i++)
 #pragma unroll
-            for (int i = 0; i < TM; i++)
+            for (int j = 0; j < TN; j++) acc[i][j] = mfma32(fa[i], fw[j], acc[i][j]);
+    };
+    constexpr int NM = TM * TN, NR = TM + TN, NI = NM < NR ? NM : NR;  // products, reads, interleaved pairs
+    auto interleave = [&]() {
 #pragma unroll
-                for (int j = 0; j < TN; j++) acc[i][j] = mfma32(fa[i], fw[j], acc[i][j]);
+        for (int g = 0; g < NI; g++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
         }
+        if (NM > NI) __builtin_amdgcn_sched_group_barrier(0x008, NM - NI, 0);
+        if (NR > NI) __builtin_amdgcn_sched_group_barrier(0x100, NR - NI, 0);
+    };
+    // tile kt from (a, w), its step-0 fragments already in (fa0, fw0); the loads of tile kt + 1 go to (an, wn_)
+    auto tile = [&](int kt, const f16* a, const f16* w, f16* an, f16* wn_) {
+        if (kt + 1 < nk) issue(kt + 1, an, wn_);
+        frags(a, w, 1, fa1, fw1);
+        mma(fa0, fw0, 0, TM);
+        __builtin_amdgcn_sched_group_barrier(0x020, AR + WR, 0);  // the next tile's loads first
+        interleave();
+        frags(a, w, 2, fa0, fw0);
+        mma(fa1, fw1, 0, TM);
+        interleave();
+        frags(a, w, 3, fa1, fw1);
+        mma(fa0, fw0, 0, TM);
+        interleave();
+        mma(fa1, fw1, 0, TM / 2);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0);  // tile kt + 1 has landed (vmcnt) and every wave is done with tile kt
+        __syncthreads();
+        if (kt + 1 < nk) frags(an, wn_, 0, fa0, fw0);
+        mma(fa1, fw1, TM / 2, TM);
+        __builtin_amdgcn_sched_barrier(0);
     };
 
     // two K tiles per iteration, one per LDS buffer (distinct arrays, so the compiler sees that the loads in flight
@@ -140,20 +174,13 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
     issue(0, sA0, sW0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    frags(sA0, sW0, 0, fa0, fw0);
     int kt = 0;
     for (; kt + 1 < nk; kt += 2) {
-        issue(kt + 1, sA1, sW1);
-        __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the products they overlap
-        compute(sA0, sW0);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (kt + 2 < nk) issue(kt + 2, sA0, sW0);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(sA1, sW1);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+        tile(kt, sA0, sW0, sA1, sW1);
+        tile(kt + 1, sA1, sW1, sA0, sW0);
     }
-    if (kt < nk) compute(sA0, sW0);
+    if (kt < nk) tile(kt, sA0, sW0, sA1, sW1);
 
     // epilogue: acc[i][j] element r is row m0 + i * 32 + 8 (r / 4) + 4 lh + r % 4, column n0 + j * 32 + lr
     const int m0 = bm * BM + wm * WM, n0 = bn * BN + wn * WN;
