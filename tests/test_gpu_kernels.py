@@ -126,6 +126,26 @@ def test_enc_attention_peaked_scores(ctx):
     assert rel_err(out, ref) < attention_bar(q, k, v, ref)
 
 
+def test_enc_attention_late_peak(ctx):
+    """Every query's largest scores far past the running max in late blocks: a peak at key 700 and a dominant one at
+    key 1490 (the padded last tile, whose keys past 1500 are masked), so each of those blocks is recomputed against
+    a raised max with O rescaled (its probabilities would sum far past 2^12, or overflow fp16, otherwise)."""
+    rng = np.random.default_rng(13)
+    q, k, v = (f16(rng, (1, 2, 1500, 64)) for _ in range(3))
+    c = np.full(64, 1.0, np.float32)
+    q = (q.astype(np.float32) + c).astype(np.float16)
+    k = k.astype(np.float32)
+    k[:, :, 700] += 3.0 * c
+    k[:, :, 1490] += 6.0 * c
+    k = k.astype(np.float16)
+    qs, q = prescaled(q)
+    out = run_attention(ctx, qs, k, v)
+    ref = attention64(q, k, v)
+    assert rel_err(out, ref) < attention_bar(q, k, v, ref)
+    # the output is dominated by v[1490] (a kernel that missed the late peak would not be)
+    assert rel_err(out, np.broadcast_to(v[:, :, 1490:1491].astype(np.float64), out.shape)) < 0.05
+
+
 def test_enc_attention_large_v3_shape(ctx):
     """8 clips x 20 heads x 1500 x 1500, head 64 (the encoder group's attention); every (clip, head) checked on 48
     query rows spread over the window, including the last ones of the padded tile."""
