@@ -16,15 +16,15 @@
 //                 GELU -> fp16, fp16, the self-attention q/k/v scatter into the cache, or logits with a masked
 //                 per-workgroup argmax (gemv_* + cuBLAS + fill_bias + kv_write, whisper.cu:92-97, 309-317, 497-567)
 //   dec_attn      attention of one query per (row, head) over a run of keys: self-attention over the cache
-//                 (whisper.cu:319-353) and cross-attention over the encoder keys/values with the alignment-head
-//                 probabilities recorded (whisper.cu:355-449)
+//                 (whisper.cu:319-353) and cross-attention over the encoder keys/values, which projects its own
+//                 query from the row's LayerNorm output and records the alignment-head probabilities
+//                 (whisper.cu:355-449)
 //   dec_add_ln    residual add of the split-K partials + bias, fused with the next LayerNorm (whisper.cu:71-82)
 //   dec_argmax    greedy choice from the per-workgroup argmax partials; advances the position (whisper.cu:451-495)
 #include "mz_common.h"
 #include "mz_kernels.h"
 
 namespace {
-
 
 // LayerNorm of one row held as v = x[4t .. 4t + 3] by thread t (threads with 4t >= dim hold zeros), written as fp16;
 // gamma / beta come in already loaded. Each wave takes the mean and the sum of squared deviations of its own
