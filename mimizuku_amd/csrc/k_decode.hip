@@ -398,9 +398,9 @@ __global__ void __launch_bounds__(256) dec_lmhead_kernel(const MzDec p, int T) {
 // loading each key's k and v rows together, and keep a private online softmax; the groups merge in LDS. Scores are
 // in the log2 domain (log2(e) / 8 folded into q), all arithmetic fp32. The alignment heads' probabilities are
 // written for position ctr[1] from the scores kept in LDS.
-// AG groups of 8 lanes per workgroup, AU keys in flight per group: the cross-attention uses 32 x 8 (every (row, head)
-// workgroup of a 32-row batch resident at once, 64 KB in flight each), the self-attention over at most 448 cached
-// positions 64 x 4 (one pass over a 200-position cache).
+// AG groups of 8 lanes per workgroup, AU keys in flight per group: 32 x 8 (every (row, head) workgroup of a 32-row
+// batch resident at once, 64 KB in flight each; one pass over a self-attention cache of up to 256 positions; 64 x 4
+// was 3 us per step slower there, its merge over twice the groups included).
 // The cross-attention's query projection runs in the same workgroup (wq set): its head's 64 rows of wq (read by the
 // 32 rows' workgroups of that head, so from L2 after the first) against the row's layer-norm output staged in LDS,
 // 8 lanes per weight row over whole 128-byte lines, with the first keys and values in flight behind them.
@@ -643,7 +643,7 @@ hipError_t mz_dec_attn_launch(hipStream_t s, const MzDecAttn& a) {
     if (a.L > 0)
         hipLaunchKernelGGL((dec_attn_kernel<32, 8>), dim3(a.B * a.nh), dim3(32 * 8), 0, s, a);
     else
-        hipLaunchKernelGGL((dec_attn_kernel<64, 4>), dim3(a.B * a.nh), dim3(64 * 8), 0, s, a);
+        hipLaunchKernelGGL((dec_attn_kernel<32, 8>), dim3(a.B * a.nh), dim3(32 * 8), 0, s, a);
     return hipGetLastError();
 }
 
