@@ -264,27 +264,44 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
         const __amdgpu_buffer_rsrc_t rO = rsrc(p.out, (unsigned)(p.M * p.ldo) * ES);
         // the row stride as an opaque scalar: each element's offset is then one vector add of a scalar row offset
         const unsigned rs = __builtin_amdgcn_readfirstlane((unsigned)p.ldo * ES);
+        auto put = [&](float v, unsigned o) {
+            if (EPI == EPI_F16) {
+                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (f16)v), rO, o, 0, 0);
+            } else if (EPI == EPI_GELU_F16) {
+                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (f16)gelu_erf(v)), rO, o, 0, 0);
+            } else {
+                const float x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rO, o, 0, 0));
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, x + v), rO, o, 0, 0);
+            }
+        };
+        // rows m0 + 4 lh + i * 32 + 8 (r / 4) + r % 4 in order: one row further, five after every fourth
+        const unsigned off0 = (unsigned)((m0 + 4 * lh) * p.ldo + n0 + lr) * ES;
+        if (n0 + WN <= p.N) {
+            // every column of the wave exists (wave-uniform): the TN column blocks of a row are stored back to back,
+            // the later ones through the instruction's immediate offset, so the two halves of a 128-byte line are
+            // written together rather than 64 stores apart
+            float bv[TN];
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int n = n0 + j * 32 + lr;
-            if (n >= p.N) continue;
-            const float bv = p.bias ? (float)p.bias[n] : 0.f;
-            // rows m0 + 4 lh + i * 32 + 8 (r / 4) + r % 4 in order: one row further, five after every fourth
-            unsigned off = (unsigned)((m0 + 4 * lh) * p.ldo + n) * ES;
+            for (int j = 0; j < TN; j++) bv[j] = p.bias ? (float)p.bias[n0 + j * 32 + lr] : 0.f;
+            unsigned off = off0;
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
-                for (int r = 0; r < 16; r++, off += (r & 3) == 0 ? 5 * rs : rs) {
-                    const float v = acc[i][j][r] + bv;
-                    if (EPI == EPI_F16) {
-                        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (f16)v), rO, off, 0, 0);
-                    } else if (EPI == EPI_GELU_F16) {
-                        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (f16)gelu_erf(v)), rO, off, 0, 0);
-                    } else {
-                        const float o = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rO, off, 0, 0));
-                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, o + v), rO, off, 0, 0);
-                    }
-                }
+                for (int r = 0; r < 16; r++, off += (r & 3) == 0 ? 5 * rs : rs)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) put(acc[i][j][r] + bv[j], off + j * 32 * ES);
+        } else {
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int n = n0 + j * 32 + lr;
+                if (n >= p.N) continue;
+                const float bv = p.bias ? (float)p.bias[n] : 0.f;
+                unsigned off = off0 + j * 32 * ES;
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++, off += (r & 3) == 0 ? 5 * rs : rs) put(acc[i][j][r] + bv, off);
+            }
         }
         return;
     }
