@@ -236,23 +236,25 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
         const int blk = n0 >> 6, c0 = (n0 & 63) + lr;
         // the encoder's q tiles are stored multiplied by log2(e) / 8, the attention's exponent scale
         const float qsc = (p.kind == 3 && blk < p.nh) ? 0.125f * 1.4426950408889634f : 1.f;
+        float bv[TN];
+#pragma unroll
+        for (int j = 0; j < TN; j++) bv[j] = (p.bias ? (float)p.bias[min(n0 + j * 32 + lr, p.N - 1)] : 0.f) * qsc;
+        // frame tb + dr >= 1500 is frame tb + dr - 1500 of the next clip
+        const unsigned wrap = (unsigned)(clip - MZ_TENC * MZ_HD);
 #pragma unroll
         for (int i = 0; i < TM; i++) {
             const int mb = m0 + i * 32 + 4 * lh, gb = mb / MZ_TENC, tb = mb - gb * MZ_TENC;
             const unsigned cb = (unsigned)((gb - g0) * clip + (long)blk * (MZ_TPAD * MZ_HD)) + c0 + tb * MZ_HD;
-            // frame tb + dr >= 1500 is frame tb + dr - 1500 of the next clip
-            const unsigned wrap = (unsigned)(clip - MZ_TENC * MZ_HD);
 #pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const int n = n0 + j * 32 + lr;
-                const float bv = (p.bias ? (float)p.bias[min(n, p.N - 1)] : 0.f) * qsc;
+            for (int r = 0; r < 16; r++) {
+                const int dr = 8 * (r >> 2) + (r & 3);
+                const unsigned e = cb + dr * MZ_HD + (tb + dr >= MZ_TENC ? wrap : 0u);
+                // a row's 32-column blocks back to back (the later ones through the immediate offset): the two halves
+                // of a 128-byte tile row are written together
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int dr = 8 * (r >> 2) + (r & 3);
-                    const unsigned e = cb + j * 32 + dr * MZ_HD + (tb + dr >= MZ_TENC ? wrap : 0u);
-                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (f16)fmaf(acc[i][j][r], qsc, bv)),
-                                                          rH, e * 2, 0, 0);
-                }
+                for (int j = 0; j < TN; j++)
+                    __builtin_amdgcn_raw_buffer_store_b16(
+                        __builtin_bit_cast(short, (f16)fmaf(acc[i][j][r], qsc, bv[j])), rH, e * 2 + j * 64, 0, 0);
             }
         }
         return;
