@@ -227,7 +227,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
         // wave's 128 rows span at most two of them (128 < 1500): the store descriptor starts at the first one's
         // tiles and ends after the second one, or after the last clip of the call, so the range check drops the
         // rows of a partial last tile. Rows of the second clip add one clip's worth of tiles; every offset stays
-        // below 2^31 bytes (two clips of at most 1024 tiles).
+        // below 2^31 bytes (two clips of at most 4096 tiles).
         const int g0 = m0 / MZ_TENC;
         const long clip = (long)p.blocks_per_clip * (MZ_TPAD * MZ_HD);
         const int ncl = min(p.M / MZ_TENC - g0, 2);
@@ -348,7 +348,9 @@ hipError_t pick(hipStream_t s, const MzGemm& g) {
 
 hipError_t mz_gemm_launch(hipStream_t s, int aload, int epi, const MzGemm& g) {
     if (g.K % 64 != 0 || g.M <= 0 || g.N <= 0 || g.K <= 0 || g.N % 4 != 0) return hipErrorInvalidValue;
-    if (epi == EPI_HEADS && (g.N % 64 != 0 || g.M % MZ_TENC != 0 || g.blocks_per_clip <= 0 || g.blocks_per_clip > 1024))
+    // (the head-scatter offsets span two clips of blocks_per_clip 1536 x 64 tiles: 4096 keeps them below 2^31 bytes;
+    // large-v3's cross k/v is 32 layers x 2 x 20 heads = 1280 tiles per clip)
+    if (epi == EPI_HEADS && (g.N % 64 != 0 || g.M % MZ_TENC != 0 || g.blocks_per_clip <= 0 || g.blocks_per_clip > 4096))
         return hipErrorInvalidValue;
     // the store descriptors address the output with 32-bit byte offsets
     if ((epi == EPI_F16 || epi == EPI_GELU_F16 || epi == EPI_RESID_F32) &&
