@@ -53,6 +53,16 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
     // the wave index through readfirstlane: wave-uniform values (tile origins, store descriptors) stay scalar
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 2, wn = wave & 3, lr = lane & 31, lh = lane >> 5;
+    // the epilogue's bias values are requested here, ahead of the operand loads, so that their round trip is hidden
+    // behind the K loop instead of stalling the products' end. One unconditional buffer load per column block (a
+    // missing bias is a descriptor of no bytes, which reads zeros): a branch would make the compiler wait for the
+    // load at once. Kept as fp16 until used.
+    const int n0 = bn * BN + wn * WN;
+    const __amdgpu_buffer_rsrc_t rB = rsrc(p.bias, p.bias ? (unsigned)p.N * 2 : 0u);
+    f16 bias_h[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+        bias_h[j] = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(rB, (unsigned)(n0 + j * 32 + lr) * 2, 0, 0));
     const int nk = p.K >> 6;
     // this lane's slot in a direct load: row lrow of an 8-row slice, 16-byte chunk lc of the row
     // (slice r of a wave starts at a multiple of 8 rows whose bit 3 is r's bit 0)
@@ -183,7 +193,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
     if (kt < nk) tile(kt, sA0, sW0, sA1, sW1);
 
     // epilogue: acc[i][j] element r is row m0 + i * 32 + 8 (r / 4) + 4 lh + r % 4, column n0 + j * 32 + lr
-    const int m0 = bm * BM + wm * WM, n0 = bn * BN + wn * WN;
+    const int m0 = bm * BM + wm * WM;
     if (EPI == EPI_HEADS) {
         if (p.kind == 3) __syncthreads();  // every wave is done reading operands: LDS is free for the v transposes
         const int blk = n0 >> 6;           // a wave's columns lie in one 64-wide head block (WN <= 64)
@@ -197,7 +207,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
             for (int i = 0; i < TM; i++) {
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
-                    const float bv = p.bias ? (float)p.bias[min(n0 + j * 32 + lr, p.N - 1)] : 0.f;
+                    const float bv = (float)bias_h[j];
 #pragma unroll
                     for (int r = 0; r < 16; r++)
                         st[(j * 32 + lr) * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)] = (f16)(acc[i][j][r] + bv);
@@ -238,7 +248,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
         const float qsc = (p.kind == 3 && blk < p.nh) ? 0.125f * 1.4426950408889634f : 1.f;
         float bv[TN];
 #pragma unroll
-        for (int j = 0; j < TN; j++) bv[j] = (p.bias ? (float)p.bias[min(n0 + j * 32 + lr, p.N - 1)] : 0.f) * qsc;
+        for (int j = 0; j < TN; j++) bv[j] = (float)bias_h[j] * qsc;
         // frame tb + dr >= 1500 is frame tb + dr - 1500 of the next clip
         const unsigned wrap = (unsigned)(clip - MZ_TENC * MZ_HD);
 #pragma unroll
@@ -284,7 +294,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
             // written together rather than 64 stores apart
             float bv[TN];
 #pragma unroll
-            for (int j = 0; j < TN; j++) bv[j] = p.bias ? (float)p.bias[n0 + j * 32 + lr] : 0.f;
+            for (int j = 0; j < TN; j++) bv[j] = (float)bias_h[j];
             unsigned off = off0;
 #pragma unroll
             for (int i = 0; i < TM; i++)
@@ -297,7 +307,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
             for (int j = 0; j < TN; j++) {
                 const int n = n0 + j * 32 + lr;
                 if (n >= p.N) continue;
-                const float bv = p.bias ? (float)p.bias[n] : 0.f;
+                const float bv = (float)bias_h[j];
                 unsigned off = off0 + j * 32 * ES;
 #pragma unroll
                 for (int i = 0; i < TM; i++)
@@ -312,7 +322,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
     for (int j = 0; j < TN; j++) {
         const int n = n0 + j * 32 + lr;
         if (n >= p.N) continue;
-        const float bv = p.bias ? (float)p.bias[n] : 0.f;
+        const float bv = (float)bias_h[j];
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll

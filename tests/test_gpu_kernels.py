@@ -212,6 +212,43 @@ def test_gemm_epilogues(ctx):
         ctx.free(p)
 
 
+def test_gemm_gelu_every_fp16_value(ctx):
+    """The GELU epilogue on every finite fp16 input: row m of x holds value m in column 0 and w is 1 there, so each
+    accumulator is exactly that value; no bias (a missing bias reads zeros). Against 0.5 v erfc(-v / sqrt 2) in float64:
+    within 1.5 fp16 ulp everywhere (the Abramowitz & Stegun erf reaches 1.28 in the tail, at v = -4.08) and correctly
+    rounded for all but a few hundred values (257 measured). Every column of a row is the same value, and the 64 columns
+    cover both the whole-block and the column-checked stores."""
+    from scipy.special import erfc
+    v = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    v = v[np.isfinite(v)]
+    m, n, k = v.size, 64, 64
+    x = np.zeros((m, k), np.float16)
+    x[:, 0] = v
+    w = np.zeros((n, k), np.float16)
+    w[:, 0] = 1
+    dx, dw = ctx.upload_new(x), ctx.upload_new(w)
+    dy = ctx.alloc(m * n * 2)
+    L.check(L.lib().mz_linear(ctx.h, linear_args(epilogue=L.EPI_GELU_F16, a=dx, lda=k, w=dw, m=m, n=n, k=k, out=dy,
+                                                 ldo=n)))
+    y = ctx.download(dy, (m, n), np.float16)
+    for p in (dx, dw, dy):
+        ctx.free(p)
+    bits = y.view(np.uint16)
+    assert (bits == bits[:, :1]).all()
+    vd = v.astype(np.float64)
+    ref = 0.5 * vd * erfc(-vd / np.sqrt(2))
+    got = y[:, 0].astype(np.float64)
+    ulp = 2.0 ** (np.maximum(np.floor(np.log2(np.maximum(np.abs(ref), 1e-300))), -14) - 10)
+    err = np.abs(got - ref) / ulp
+    sub = np.abs(vd) < 2.0 ** -14  # fp16 subnormal inputs (and zeros)
+    worst = int(np.argmax(err))
+    print("GELU over %d fp16 values: max %.3f ulp at v = %g; %d not correctly rounded" %
+          (v.size, err[worst], vd[worst], int((y[:, 0] != ref.astype(np.float16)).sum())))
+    assert err[~sub].max() <= 1.5, ("normal inputs", vd[~sub][np.argmax(err[~sub])])
+    assert err[sub].max() <= 1.5, ("subnormal inputs", vd[sub][np.argmax(err[sub])])
+    assert (y[:, 0] != ref.astype(np.float16)).sum() < 1000
+
+
 @pytest.mark.parametrize("kind", [3, 2])
 def test_gemm_head_scatter(ctx, kind):
     """kind 3: [q|k|v][head] tiles of the encoder self-attention (v tiles transposed, q tiles multiplied by
