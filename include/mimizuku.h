@@ -92,7 +92,8 @@ typedef struct {
     /* MZ_EPI_HEADS: column n -> block n / 64, row m -> clip m / 1500, time m % 1500; the block's tile is at
      * heads + ((slot0 + clip) * blocks_per_clip + block) * 1536 * 64 halves. kind 3: blocks [q|k|v][head] (encoder
      * self-attention; the q tiles stored multiplied by log2(e) / 8, the v tiles transposed [64][1536]), kind 2:
-     * [layer][k|v][head] (cross-attention; every tile row-major [1536][64]). */
+     * [layer][k|v][head] (cross-attention; every tile row-major [1536][64]). Requires n % 64 == 0, m a whole number
+     * of clips and 1 <= blocks_per_clip <= 4096 (large-v3's cross k/v: 32 x 2 x 20 = 1280). */
     uint64_t heads;
     int blocks_per_clip, nh, kind, slot0;
     /* implicit conv1d (kernel 3, padding 1): A[clip * conv_tout + t][tap * cin + ci] =
