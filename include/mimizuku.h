@@ -138,7 +138,9 @@ typedef struct {
 /* Device bytes the engine allocates besides the weights (scratch_bytes, src/model.rs:324-330). */
 size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int eg);
 /* Validates the geometry (Dims::load checks, src/model.rs:47-59) and allocates the engine for bmax decoded rows and
- * eg clips per encoder pass (Engine::new, src/model.rs:333-514, minus reading files). */
+ * eg clips per encoder pass (Engine::new, src/model.rs:333-514, minus reading files). Beyond the reference's limits
+ * this build needs d % 128 == 0 and d <= 1280 (every Whisper size; larger widths are refused with MZ_ERR_ARG);
+ * bmax has no upper limit besides memory, as the reference's --batch. */
 int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, int bmax, int eg, mz_engine** out);
 #define MZ_DT_F16 0
 #define MZ_DT_F32 1
@@ -331,6 +333,11 @@ int mz_cli(int argc, const char* const* argv);
 /* Token start times from alignment-head weights w [rows][heads][cols_full] (f32), cropped to cols frames
  * (jump_times, src/align.rs:8-63); out[rows]. */
 int mz_jump_times(const float* w, int rows, int heads, int cols_full, int cols, int width, int half, float* out);
+/* The cost jump_times hands to the DTW (src/align.rs:14-52): m[i][j] = minus the head average of the width-`width`
+ * median-filtered per-column z-scores of w [rows][heads][cols_full] cropped to cols columns (rows, cols >= 1).
+ * half != 0 is align.rs's arithmetic: column sums in float in row order, fp16 roundings of the mean, deviation,
+ * z-scores and average; half == 0 takes the column sums in double and rounds nothing. */
+int mz_align_cost(const float* w, int rows, int heads, int cols_full, int cols, int width, int half, double* m);
 /* Dynamic time warping on cost m [rows][cols] (dtw, src/align.rs:66-106); path written to text/time (capacity
  * rows + cols), its length to *len. */
 int mz_dtw(const double* m, int rows, int cols, int32_t* text, int32_t* time, int32_t* len);

@@ -123,6 +123,7 @@ SIGNATURES = {
     "mz_results_json": (i32, [P, P, i32, P, P, P, i32, P, P, P, sz, C.POINTER(sz)]),
     "mz_cli": (i32, [i32, P]),
     "mz_jump_times": (i32, [P, i32, i32, i32, i32, i32, i32, P]),
+    "mz_align_cost": (i32, [P, i32, i32, i32, i32, i32, i32, P]),
     "mz_jump_times_device": (i32, [P, u64, C.c_int64, i32, P, P, i32, i32, i32, i32, P, C.c_int64]),
     "mz_dtw": (i32, [P, i32, i32, P, P, P]),
     "mz_f2h": (C.c_uint16, [f32]),

@@ -143,39 +143,48 @@ inline float median7(const float* p) {
     return a[3];
 }
 
-// Token start times (src/align.rs:8-63) from w [rows][heads][cols_full].
+// The DTW cost of jump_times (src/align.rs:8-52): m [rows][cols] = minus the head average of the median-filtered
+// per-column z-scores of w [rows][heads][cols_full] cropped to cols columns (rows, cols >= 1).
 template <class T>
-void jump_times_impl(const T* w, int rows, int heads, int cols_full, int cols, int width, int half, float* out) {
-    if (rows == 0) return;
-    if (cols == 0) {
-        std::fill(out, out + rows, 0.f);
-        return;
-    }
+void align_cost_impl(const T* w, int rows, int heads, int cols_full, int cols, int width, int half, double* m) {
     const int pad = width / 2;
     std::vector<float> avg((size_t)rows * cols, 0.f), z((size_t)rows * cols), win(width), padded(cols + 2 * pad);
     std::vector<double> sum(cols), sq(cols);
-    std::vector<float> mean(cols), sd(cols);
+    std::vector<float> sumf(cols), sqf(cols), mean(cols), sd(cols);
     for (int a = 0; a < heads; a++) {
-        // normalise each column over the rows (population std); a constant column scores 0
+        // normalise each column over the rows (population std); a constant column scores 0. half: the column sum and
+        // the sum of squared deviations from the unrounded mean accumulate in float in row order, then the mean and
+        // deviation are rounded through fp16 (src/align.rs:18-20); otherwise both sums are taken in double
         std::fill(sum.begin(), sum.end(), 0.0);
         std::fill(sq.begin(), sq.end(), 0.0);
+        std::fill(sumf.begin(), sumf.end(), 0.f);
+        std::fill(sqf.begin(), sqf.end(), 0.f);
         for (int i = 0; i < rows; i++) {
             const size_t o = ((size_t)i * heads + a) * cols_full;
-            for (int j = 0; j < cols; j++) sum[j] += load_w(w, o + j);
+            if (half)
+                for (int j = 0; j < cols; j++) sumf[j] += load_w(w, o + j);
+            else
+                for (int j = 0; j < cols; j++) sum[j] += load_w(w, o + j);
         }
-        for (int j = 0; j < cols; j++) mean[j] = (float)(sum[j] / rows);
+        for (int j = 0; j < cols; j++) mean[j] = half ? sumf[j] / (float)rows : (float)(sum[j] / rows);
         for (int i = 0; i < rows; i++) {
             const size_t o = ((size_t)i * heads + a) * cols_full;
             for (int j = 0; j < cols; j++) {
-                const double dv = (double)(load_w(w, o + j) - mean[j]);
-                sq[j] += dv * dv;
+                if (half) {
+                    const float dv = load_w(w, o + j) - mean[j];
+                    sqf[j] += dv * dv;
+                } else {
+                    const double dv = (double)(load_w(w, o + j) - mean[j]);
+                    sq[j] += dv * dv;
+                }
             }
         }
         for (int j = 0; j < cols; j++) {
-            sd[j] = std::sqrt((float)(sq[j] / rows));
             if (half) {
+                sd[j] = rhw(std::sqrt(sqf[j] / (float)rows));
                 mean[j] = rhw(mean[j]);
-                sd[j] = rhw(sd[j]);
+            } else {
+                sd[j] = std::sqrt((float)(sq[j] / rows));
             }
         }
         for (int i = 0; i < rows; i++) {
@@ -213,12 +222,23 @@ void jump_times_impl(const T* w, int rows, int heads, int cols_full, int cols, i
             }
         }
     }
-    std::vector<double> m((size_t)rows * cols);
-    for (size_t k = 0; k < m.size(); k++) {
+    for (size_t k = 0; k < (size_t)rows * cols; k++) {
         float s = avg[k] / (float)heads;
         if (half) s = rhw(s);
         m[k] = -(double)s;
     }
+}
+
+// Token start times (src/align.rs:8-63) from w [rows][heads][cols_full].
+template <class T>
+void jump_times_impl(const T* w, int rows, int heads, int cols_full, int cols, int width, int half, float* out) {
+    if (rows == 0) return;
+    if (cols == 0) {
+        std::fill(out, out + rows, 0.f);
+        return;
+    }
+    std::vector<double> m((size_t)rows * cols);
+    align_cost_impl(w, rows, heads, cols_full, cols, width, half, m.data());
     std::vector<int> text, time;
     dtw_path(m.data(), rows, cols, text, time);
     int n = 0;
@@ -237,6 +257,15 @@ static bool jump_args_ok(int rows, int heads, int cols_full, int cols, int width
 static int host_ok() {
     static const bool ok = __builtin_cpu_supports("f16c") && __builtin_cpu_supports("avx2");
     return ok ? MZ_OK : mz_fail(MZ_ERR_STATE, "token timestamps need a host CPU with F16C and AVX2");
+}
+
+extern "C" int mz_align_cost(const float* w, int rows, int heads, int cols_full, int cols, int width, int half,
+                             double* m) {
+    if (!w || !m || rows <= 0 || cols <= 0 || !jump_args_ok(rows, heads, cols_full, cols, width))
+        return mz_fail(MZ_ERR_ARG, "mz_align_cost: bad argument");
+    if (int r = host_ok()) return r;
+    align_cost_impl(w, rows, heads, cols_full, cols, width, half, m);
+    return MZ_OK;
 }
 
 extern "C" int mz_jump_times(const float* w, int rows, int heads, int cols_full, int cols, int width, int half,

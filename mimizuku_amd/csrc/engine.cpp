@@ -3,7 +3,7 @@
 // reset, detect, step}) and src/transcribe.rs (transcribe), with its own kernels and data layouts:
 //   * the residual streams are fp32 (encoder [clips*1500][d], decoder [bmax][d]); GEMM operands are fp16;
 //   * encoder q/k/v and every decoder layer's cross k/v are stored per head as 1536 x 64 tiles, v transposed;
-//   * the self-attention cache is per (row, head): k [max_t][64], v transposed [64][max_t].
+//   * the self-attention cache is per (row, head): k and v both [max_t][64] (one 128-byte row per position).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -197,13 +197,14 @@ extern "C" size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int 
 extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, int bmax, int eg, mz_engine** out) {
     if (!c || !d || !g || !out) return mz_fail(MZ_ERR_ARG, "mz_engine_new: null argument");
     *out = nullptr;
-    // geometry limits (Dims::load, src/model.rs:47-59) plus this build's: rows of dim % 128 == 0 and <= 2048
-    if (d->nh * HD != d->d || d->d % 128 || d->d > 2048 || d->ff % 64 || d->ff <= 0 || d->n_mels % 8 ||
+    // geometry limits (Dims::load, src/model.rs:47-59) plus this build's: d % 128 == 0 and d <= 1280 (the decoder's
+    // unsplit products, the LM head and the cross-attention's query projection hold a whole row of K in LDS)
+    if (d->nh * HD != d->d || d->d % 128 || d->d > MZ_DEC_KSLICE || d->ff % 64 || d->ff <= 0 || d->n_mels % 8 ||
         d->n_mels <= 0 || d->max_t < 16 || d->max_t > 448 || d->max_t % 8 || d->enc_layers < 1 || d->enc_layers > 64 ||
         d->dec_layers < 1 || d->dec_layers > 64 || d->vocab <= 0)
         return mz_fail(MZ_ERR_ARG,
                        "unsupported shape d=%d ff=%d nh=%d n_mels=%d max_t=%d layers=%d/%d: the kernels need 64-wide "
-                       "heads, d %% 128 == 0 (<= 2048), ff %% 64 == 0, n_mels %% 8 == 0, max_t %% 8 == 0 in [16, 448]",
+                       "heads, d %% 128 == 0 (<= 1280), ff %% 64 == 0, n_mels %% 8 == 0, max_t %% 8 == 0 in [16, 448]",
                        d->d, d->ff, d->nh, d->n_mels, d->max_t, d->enc_layers, d->dec_layers);
     if (bmax <= 0 || eg <= 0 || eg > bmax) return mz_fail(MZ_ERR_ARG, "bmax %d / enc group %d", bmax, eg);
     if (g->n_begin_suppress > 2) return mz_fail(MZ_ERR_ARG, "more than two begin_suppress tokens are not supported");

@@ -1,9 +1,10 @@
 // Token timestamps on the device: the alignment heads' cross-attention rows of every clip -> per-column z-scores ->
 // median filter over time -> mean over heads -> dynamic time warping -> the time of each token's first frame.
 // Follows src/align.rs:8-106 (transformers' _extract_token_timestamps) and computes exactly what the host routine
-// mz_jump_times computes: the column statistics are accumulated in double in row order, every binary16 round trip is
-// a round-to-nearest-even conversion, the DTW cost cells are (float)(-(double)s + (double)c), and contraction into
-// fused multiply-adds is off, so both give identical bits.
+// mz_jump_times computes: the column statistics are accumulated in row order (in float with the fp16 roundings, as
+// src/align.rs:18-23 does, or in double without them), every binary16 round trip is a round-to-nearest-even
+// conversion, the DTW cost cells are (float)(-(double)s + (double)c), and contraction into fused multiply-adds is
+// off, so both give identical bits.
 //
 // Three launches per batch of clips:
 //   ts_stats_kernel  one thread per (clip, head, column): mean and population standard deviation over the rows
@@ -47,19 +48,29 @@ __global__ void __launch_bounds__(256) ts_stats_kernel(const MzTs p) {
     if (j >= C || R <= 0) return;
     const float* w = p.w + c * p.clip_stride + (long)a * p.cols_full + j;
     const long rs = (long)p.heads * p.cols_full;
-    double sum = 0.0;
-    for (int i = 0; i < R; i++) sum += (double)w[i * rs];
-    const float mean = (float)(sum / R);
-    double sq = 0.0;
-    for (int i = 0; i < R; i++) {
-        const double dv = (double)(w[i * rs] - mean);
-        sq += dv * dv;
-    }
-    float sd = __builtin_sqrtf((float)(sq / R));
-    float mu = mean;
+    float mu, sd;
     if (p.half) {
-        mu = rh(mu);
-        sd = rh(sd);
+        float sum = 0.f;
+        for (int i = 0; i < R; i++) sum += w[i * rs];
+        const float mean = sum / (float)R;
+        float sq = 0.f;
+        for (int i = 0; i < R; i++) {
+            const float dv = w[i * rs] - mean;
+            sq += dv * dv;
+        }
+        mu = rh(mean);
+        sd = rh(__builtin_sqrtf(sq / (float)R));
+    } else {
+        double sum = 0.0;
+        for (int i = 0; i < R; i++) sum += (double)w[i * rs];
+        const float mean = (float)(sum / R);
+        double sq = 0.0;
+        for (int i = 0; i < R; i++) {
+            const double dv = (double)(w[i * rs] - mean);
+            sq += dv * dv;
+        }
+        mu = mean;
+        sd = __builtin_sqrtf((float)(sq / R));
     }
     const long o = ((long)c * p.heads + a) * p.cols_full + j;
     p.mean[o] = mu;

@@ -254,8 +254,8 @@ __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
 
 // ---------------------------------------------------------------- LM head
 
-// Logits of <= 32 rows over the whole vocabulary, with each workgroup's masked argmax per row. The workgroup keeps
-// its rows' x in registers (the B operands of 16x16x32 products, its quarter of K per wave) and streams a contiguous
+// Logits of 32 rows (row block blockIdx.y) over the whole vocabulary, with each workgroup's masked argmax per row. The
+// workgroup keeps its rows' x in registers (the B operands of 16x16x32 products, its quarter of K per wave) and streams a contiguous
 // run of 16-column weight tiles through a 3-deep LDS ring (direct loads, two tiles in flight), so x is read once per
 // workgroup and the weight stream never waits for a round trip per tile. Ids and the argmax rules as dec_gemm's.
 constexpr int LM_TILE = 16;                          // vocabulary ids per tile
@@ -268,7 +268,7 @@ __global__ void __launch_bounds__(256) dec_lmhead_kernel(const MzDec p, int T) {
     float(*red)[32][LM_TILE + 1] = (float(*)[32][LM_TILE + 1])(lds + 3 * LM_TB / 2);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lq = lane >> 4;
     const int G = p.K >> 6, ntiles = (p.N + LM_TILE - 1) / LM_TILE;
-    const int t0 = blockIdx.x * T, nt = min(T, ntiles - t0);
+    const int t0 = blockIdx.x * T, nt = min(T, ntiles - t0), m0 = blockIdx.y * 32;
     const int r8 = lane >> 3, q8 = lane & 7;
     const int pos = p.ctr[1];
     const bool first = pos + 1 == p.prompt_len;
@@ -287,7 +287,8 @@ __global__ void __launch_bounds__(256) dec_lmhead_kernel(const MzDec p, int T) {
     }
 
     // x rows (32 x K) through LDS into this wave's fragments: groups g = wave + 4 i, halves s of 32 k, row halves h
-    const __amdgpu_buffer_rsrc_t rX = rsrc(p.x, (unsigned)p.M * (unsigned)p.ldx * 2u);
+    // rows past M read zeros through the descriptor's range check
+    const __amdgpu_buffer_rsrc_t rX = rsrc(p.x + (long)m0 * p.ldx, (unsigned)min(p.M - m0, 32) * (unsigned)p.ldx * 2u);
     for (int i = wave; i < 4 * G; i += 4) {
         const int g = i >> 2, rg = i & 3, c = q8 ^ r8 ^ (rg & 1);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rX, LDSP(lds + i * 512), 16,
@@ -372,8 +373,8 @@ __global__ void __launch_bounds__(256) dec_lmhead_kernel(const MzDec p, int T) {
         for (int e = 0; e < 2; e++) {
             const int n = n0 + ec + e;
             const float v = red[0][em][ec + e] + red[1][em][ec + e] + red[2][em][ec + e] + red[3][em][ec + e];
-            if (em < p.M && n < p.N) {
-                ((float*)p.out)[(long)em * p.ldo + n] = v;
+            if (m0 + em < p.M && n < p.N) {
+                ((float*)p.out)[(long)(m0 + em) * p.ldo + n] = v;
                 const bool masked = ((smask >> (2 * t + e)) & 1u) || (first && (n == p.bs1 || n == p.bs2));
                 if (!masked && (v > best || (v == best && n < bi))) {
                     best = v;
@@ -383,11 +384,11 @@ __global__ void __launch_bounds__(256) dec_lmhead_kernel(const MzDec p, int T) {
         }
     }
     group8_argmax(best, bi);  // the 8 threads of one row are adjacent lanes
-    if ((tid & 7) == 0 && em < p.M) {
+    if ((tid & 7) == 0 && m0 + em < p.M) {
         int2 r;
         r.x = __float_as_int(best);
         r.y = bi;
-        ((int2*)p.amax)[(long)blockIdx.x * p.M + em] = r;
+        ((int2*)p.amax)[(long)blockIdx.x * p.M + m0 + em] = r;
     }
 #endif
 }
@@ -609,7 +610,7 @@ hipError_t mz_dec_gemm_launch(hipStream_t s, int epi, const MzDec& g) {
         g.K / g.ksplit > MZ_DEC_KSLICE || g.ldx % 8 != 0)
         return hipErrorInvalidValue;
     if (epi == DEPI_QKV && (g.N != 3 * g.d || g.d % 64 != 0 || !g.kc || !g.vc || !g.ctr)) return hipErrorInvalidValue;
-    if (epi == DEPI_LOGITS && (!g.sup || !g.amax || !g.ctr || g.M > 32 || g.N > 65536)) return hipErrorInvalidValue;
+    if (epi == DEPI_LOGITS && (!g.sup || !g.amax || !g.ctr || g.N > 65536 || g.K > MZ_DEC_KSLICE)) return hipErrorInvalidValue;
     if (epi != DEPI_PARTIAL && g.ksplit != 1) return hipErrorInvalidValue;
     const dim3 grid((g.N + 31) / 32, g.ksplit, (g.M + 31) / 32);
     const int ksl = g.K / g.ksplit;
@@ -627,7 +628,7 @@ hipError_t mz_dec_gemm_launch(hipStream_t s, int epi, const MzDec& g) {
         case DEPI_F16: hipLaunchKernelGGL((dec_gemm_kernel<DEPI_F16, MZ_DEC_KSLICE>), grid, dim3(256), 0, s, g); break;
         case DEPI_LOGITS: {
             const int T = mz_lm_tiles_per_block(g.N);
-            hipLaunchKernelGGL(dec_lmhead_kernel, dim3(mz_lm_blocks(g.N)), dim3(256), 0, s, g, T);
+            hipLaunchKernelGGL(dec_lmhead_kernel, dim3(mz_lm_blocks(g.N), (g.M + 31) / 32), dim3(256), 0, s, g, T);
             break;
         }
         default: return hipErrorInvalidValue;

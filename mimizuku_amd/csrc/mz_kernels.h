@@ -66,7 +66,7 @@ enum MzDecEpi {
     DEPI_PARTIAL = 0,  // part[ks][m][n] (f32), ks = blockIdx.y (split-K)
     DEPI_GELU_F16 = 1, // out f16 [m][ldo] = gelu(acc + bias)
     DEPI_LOGITS = 2,   // out f32 [m][ldo] = acc, and amax[wg][m] = masked (max, lowest id) of each workgroup's ids
-                       // (mz_lm_blocks(N) workgroups; M <= 32, K <= MZ_DEC_KSLICE)
+                       // (mz_lm_blocks(N) workgroups per 32-row block; K <= MZ_DEC_KSLICE)
     DEPI_QKV = 3,      // q -> out f32 [m][d] (+bias); k, v (+bias) -> self cache rows at position ctr[1]
     DEPI_F16 = 4,      // out f16 [m][ldo] = acc + bias
 };

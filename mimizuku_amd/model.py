@@ -316,9 +316,10 @@ class Engine:
         check(L.lib().mz_engine_buffer(self.h, which, C.byref(p), C.byref(n)))
         return p.value, n.value
 
-    def read(self, which: int, dtype, shape) -> np.ndarray:
+    def read(self, which: int, dtype, shape, offset: int = 0) -> np.ndarray:
+        """An array of `shape` read from an engine buffer at byte offset `offset` (after the stream's work)."""
         out = np.empty(shape, dtype)
-        check(L.lib().mz_engine_read(self.h, which, ptr(out), 0, out.nbytes))
+        check(L.lib().mz_engine_read(self.h, which, ptr(out), offset, out.nbytes))
         return out
 
     def tokens(self) -> np.ndarray:

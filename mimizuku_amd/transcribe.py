@@ -106,6 +106,15 @@ def jump_times(w: np.ndarray, cols: int, width: int = 7, half: bool = True) -> n
     return out
 
 
+def align_cost(w: np.ndarray, cols: int, width: int = 7, half: bool = True) -> np.ndarray:
+    """The cost jump_times hands to the DTW, float64 [rows][cols] (src/align.rs:14-52)."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, heads, full = w.shape
+    out = np.zeros((rows, cols), np.float64)
+    check(L.lib().mz_align_cost(ptr(w), rows, heads, full, cols, width, int(half), ptr(out)))
+    return out
+
+
 def jump_times_device(ctx, w: int, clip_stride: int, rows, cols, heads: int, cols_full: int, width: int = 7,
                       half: bool = True) -> list[np.ndarray]:
     """Token start times of several clips on the device (the same bits as jump_times per clip): clip c's weights are

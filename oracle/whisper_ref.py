@@ -349,20 +349,40 @@ def dtw(m: np.ndarray):
 
 def jump_times(w: np.ndarray, cols: int, width: int = 7, half: bool = False) -> np.ndarray:
     """Start time (s) of each row from alignment-head weights w [rows][heads][cols_full]
-    (TF/generation_whisper.py:241-379 `_extract_token_timestamps`; src/align.rs:8-63).
-
-    Columns are cropped to `cols` (= audio frames // 2), each head is normalised over rows, median-filtered over
-    time, the heads are averaged and DTW runs on minus the average. half=True rounds through fp16 where a model run
-    in fp16 does (src/align.rs:20-23, 52); half=False is the fp32 model's arithmetic. A constant column scores 0
-    (the fp32/fp16 model divides by zero there, src/align.rs:22).
-    """
-    rows, heads, _ = w.shape
+    (TF/generation_whisper.py:241-379 `_extract_token_timestamps`; src/align.rs:8-63): DTW over align_cost."""
+    rows = w.shape[0]
     if cols == 0:
         return np.zeros(rows, np.float32)
+    text, time = dtw(align_cost(w, cols, width, half))
+    jumps = np.concatenate([[True], np.diff(text) != 0])
+    out = (time[jumps] * 0.02).astype(np.float32)
+    if len(out) < rows:  # degenerate scores bend the path (src/align.rs:60-61)
+        out = np.concatenate([out, np.full(rows - len(out), out[-1] if len(out) else 0, np.float32)])
+    return out[:rows]
+
+
+def align_cost(w: np.ndarray, cols: int, width: int = 7, half: bool = False) -> np.ndarray:
+    """The DTW cost of jump_times, float64 [rows][cols] (src/align.rs:14-52).
+
+    Columns are cropped to `cols` (= audio frames // 2), each head is normalised over rows, median-filtered over
+    time, the heads are averaged and DTW runs on minus the average. half=True is src/align.rs:18-23, 52 exactly: the
+    column sum and the sum of squared deviations from the unrounded mean accumulate in float32 in row order (a
+    sequential fold, np.add.accumulate), then the mean, the deviation and every z-score are rounded through fp16, as
+    a model run in fp16 does. half=False is the fp32 model's arithmetic with the two sums taken in float64. A
+    constant column scores 0 (the fp32/fp16 model divides by zero there, src/align.rs:22).
+    """
+    rows, heads, _ = w.shape
     x = w[:, :, :cols].astype(np.float32)
-    mean = x.mean(0, keepdims=True, dtype=np.float64).astype(np.float32)
-    var = ((x - mean).astype(np.float64) ** 2).mean(0, keepdims=True).astype(np.float32)
-    std = np.sqrt(var)
+    if half:
+        n = np.float32(rows)
+        mean = np.add.accumulate(x, axis=0, dtype=np.float32)[-1:] / n
+        dev = (x - mean).astype(np.float32)
+        var = np.add.accumulate(dev * dev, axis=0, dtype=np.float32)[-1:] / n
+        std = np.sqrt(var.astype(np.float32))
+    else:
+        mean = x.mean(0, keepdims=True, dtype=np.float64).astype(np.float32)
+        var = ((x - mean).astype(np.float64) ** 2).mean(0, keepdims=True).astype(np.float32)
+        std = np.sqrt(var)
     if half:
         mean, std = rh(mean), rh(std)
         num = rh(x - mean)
@@ -373,12 +393,7 @@ def jump_times(w: np.ndarray, cols: int, width: int = 7, half: bool = False) -> 
     avg = z.astype(np.float32).sum(0, dtype=np.float32) / np.float32(heads)
     if half:
         avg = rh(avg)
-    text, time = dtw(-avg.astype(np.float64))
-    jumps = np.concatenate([[True], np.diff(text) != 0])
-    out = (time[jumps] * 0.02).astype(np.float32)
-    if len(out) < rows:  # degenerate scores bend the path (src/align.rs:60-61)
-        out = np.concatenate([out, np.full(rows - len(out), out[-1] if len(out) else 0, np.float32)])
-    return out[:rows]
+    return -avg.astype(np.float64)
 
 
 def token_timestamps(probs_rows: np.ndarray, align_heads, n_prompt: int, n_seq: int, frames: int,

@@ -23,3 +23,11 @@ def pytest_collection_modifyitems(config, items):
     for it in items:
         if "gpu" in it.keywords:
             it.add_marker(skip)
+
+
+@pytest.fixture(scope="session")
+def large_v3_weights():
+    """Seeded random-init weights of the full large-v3 geometry (1.5 G parameters, fp16), drawn once per session for
+    the GPU tests that run the whole model."""
+    from mimizuku_amd import synth
+    return synth.random_weights(synth.LARGE_V3, seed=8, bias_std=0.02, ln_std=0.1)

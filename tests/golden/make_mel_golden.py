@@ -3,7 +3,7 @@
 Run in the build container only (transformers 5.15.0 installed; the GPU box never runs this):
     PYTHONPATH=. python tests/golden/make_mel_golden.py
 
-The waveforms are synthetic and regenerated from `waveform(seed, seconds)` below: a chirp plus a tone plus noise,
+The waveforms are synthetic and regenerated from `waves.waveform(seed, seconds)`: a chirp plus a tone plus noise,
 amplitude 0.5. Each fixture holds the seed and length, the 80- or 128-bin features of the default (torch) path at
 the frames `cols` (every frame of the live part for short clips, every 7th for the 30 s one), the largest
 difference between the numpy and torch paths, and the attention-mask frame count.
@@ -14,16 +14,10 @@ import numpy as np
 import torch
 from transformers import WhisperFeatureExtractor
 
+from waves import waveform
+
 HERE = os.path.dirname(os.path.abspath(__file__))
 CASES = {"mel80_7s": (80, 11, 7.3), "mel128_30s": (128, 12, 30.0), "mel128_short": (128, 13, 0.9)}
-
-
-def waveform(seed: int, seconds: float) -> np.ndarray:
-    rng = np.random.default_rng(seed)
-    t = np.arange(int(16000 * seconds)) / 16000.0
-    y = 0.3 * np.sin(2 * np.pi * (200 + 300 * t) * t) + 0.1 * np.sin(2 * np.pi * 2500 * t) \
-        + 0.05 * rng.standard_normal(len(t))
-    return (0.5 * y / max(1e-9, np.abs(y).max())).astype(np.float32)
 
 
 def main():

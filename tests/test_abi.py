@@ -110,6 +110,69 @@ def test_jump_times_match_oracle_on_softmax_weights(half):
                                       R.jump_times(w, cols if cols <= 64 else 64, 7, half))
 
 
+def align_rs_cost(w, cols, width, f64_sums=False):
+    """src/align.rs:14-52 line by line with float32 scalars (the fp16 mode the reference always runs): sequential
+    float sums over the rows, fp16 roundings of the mean, the deviation and the z-scores, a sorted window for the
+    median, float sums over the heads. f64_sums takes the two column sums in float64 instead (the variant the
+    fp16 mode must not be)."""
+    f = np.float32
+    rh = lambda x: f(np.float16(f(x)))  # noqa: E731
+    rows, heads, _ = w.shape
+    pad = width // 2
+    avg = np.zeros((rows, cols), np.float32)
+    for a in range(heads):
+        z = np.zeros((rows, cols), np.float32)
+        for j in range(cols):
+            col = [f(w[i, a, j]) for i in range(rows)]
+            if f64_sums:
+                mean_f = f(sum(float(x) for x in col) / rows)
+                var = f(sum(float(f(x - mean_f)) ** 2 for x in col) / rows)
+            else:
+                acc = f(0)
+                for x in col:
+                    acc = f(acc + x)
+                mean_f = f(acc / f(rows))
+                acc = f(0)
+                for x in col:
+                    d = f(x - mean_f)
+                    acc = f(acc + f(d * d))
+                var = f(acc / f(rows))
+            mean, std = rh(mean_f), rh(np.sqrt(var))
+            for i in range(rows):
+                z[i, j] = rh(f(rh(f(col[i] - mean)) / std)) if std > 0 else f(0)
+        for i in range(rows):
+            for j in range(cols):
+                if cols <= pad:
+                    v = z[i, j]
+                else:
+                    idx = [abs(j + k - pad) for k in range(width)]
+                    idx = [t if t < cols else 2 * (cols - 1) - t for t in idx]
+                    v = sorted(z[i, t] for t in idx)[pad]
+                avg[i, j] = f(avg[i, j] + v)
+    return -np.array([[float(rh(f(avg[i, j] / f(heads)))) for j in range(cols)] for i in range(rows)])
+
+
+def test_align_cost_is_align_rs_arithmetic():
+    """The fp16 mode's cost, library and oracle, equals align.rs's own arithmetic bit for bit (brute force on small
+    inputs), including a column built so that float32 sequential sums and float64 sums round the mean to different
+    fp16 values: 4 + 2^-9 followed by three 2^-23 terms that a float32 running sum drops (mean 1 + 2^-11, an fp16
+    tie, rounds to 1.0) while float64 keeps them (rounds up to 1 + 2^-10)."""
+    rng = np.random.default_rng(5)
+    for rows, heads, cols, width in [(4, 1, 3, 1), (5, 2, 9, 7), (3, 3, 2, 7), (6, 2, 20, 15), (1, 1, 5, 7)]:
+        s = rng.standard_normal((rows, heads, cols + 3)) * 3
+        w = np.exp(s - s.max(-1, keepdims=True))
+        w = (w / w.sum(-1, keepdims=True)).astype(np.float32)
+        if (rows, width) == (4, 1):
+            w[:, 0, 0] = [4 + 2.0 ** -9, 2.0 ** -23, 2.0 ** -23, 2.0 ** -23]
+        ref = align_rs_cost(w, cols, width)
+        np.testing.assert_array_equal(R.align_cost(w, cols, width, half=True), ref)
+        np.testing.assert_array_equal(transcribe.align_cost(w, cols, width, half=True), ref)
+        np.testing.assert_array_equal(transcribe.align_cost(w, cols, width, half=False),
+                                      R.align_cost(w, cols, width, half=False))
+        if (rows, width) == (4, 1):
+            assert not np.array_equal(align_rs_cost(w, cols, width, f64_sums=True)[:, 0], ref[:, 0])
+
+
 def test_jump_times_of_the_golden_weights():
     fx = np.load(os.path.join(ROOT, "tests", "golden", "tiny_hfinit.npz"))
     w = fx["align_w"][0].transpose(1, 0, 2)[4:]

@@ -15,7 +15,7 @@ from oracle import audio_ref as A
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 sys.path.insert(0, GOLDEN)
-from make_mel_golden import waveform  # noqa: E402
+from waves import waveform  # noqa: E402
 
 
 def wav(fmt, ch, sr, bits, data: bytes) -> bytes:

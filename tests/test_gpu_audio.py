@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 sys.path.insert(0, GOLDEN)
-from make_mel_golden import waveform  # noqa: E402
+from waves import waveform  # noqa: E402
 
 NS = 480000
 

@@ -130,7 +130,8 @@ def test_decoder_layer_local(ctx, case):
     """Every decoder layer layer-local at every teacher-forced position: the oracle's layer applied to the engine's own
     fp32 residual entering it, with the engine's own (fp16) self-attention cache of the earlier positions and its
     cross keys / values, against the residual the engine produced, max-abs <= 2e-3 x RMS; the new cache rows
-    against the oracle's k / v within fp16 rounding."""
+    against the oracle's k / v within fp16 rounding; the logits against the final LayerNorm and the tied LM head
+    applied to the engine's own final residual, 2e-3 x RMS."""
     e = case.engine(ctx)
     e.set_trace(True)
     e.encode(case.mel, 0)
@@ -139,10 +140,15 @@ def test_decoder_layer_local(ctx, case):
     e.reset(seq)
     n, nh, nl = case.n, G.nh, G.dec_layers
     xkv = e.xkv()[:n].astype(np.float32)
-    worst = worst_kv = 0.0
+    worst = worst_kv = worst_lg = 0.0
+    W = case.Wf
     for p in range(T - 1):
         e.step(n, False, T)
         tr = e.dec_trace()[:, :n]
+        h = R.layer_norm(tr[nl], W["model.decoder.layer_norm.weight"], W["model.decoder.layer_norm.bias"])
+        err = rel_err(e.logits()[:n], R.linear(h, W["model.decoder.embed_tokens.weight"]))
+        worst_lg = max(worst_lg, err)
+        assert err <= TOL, (p, "logits", err)
         kc, vc = e.self_kv()
         for i in range(nl):
             cache = [(kc[i, b, :, :p].astype(np.float32), vc[i, b, :, :p].astype(np.float32)) if p else (None, None)
@@ -155,15 +161,18 @@ def test_decoder_layer_local(ctx, case):
             for got, ref in ((kc[i, :n, :, p], k), (vc[i, :n, :, p], v)):
                 ref = ref.reshape(n, nh, 64)
                 worst_kv = max(worst_kv, float(np.abs(got.astype(np.float32) - ref).max() / np.sqrt((ref ** 2).mean())))
-    print(case.name, "decoder layer-local max-abs / RMS", worst, "new k/v", worst_kv)
+    print(case.name, "decoder layer-local max-abs / RMS", worst, "new k/v", worst_kv, "LM head", worst_lg)
     assert worst_kv <= TOL
     e.close()
 
 
-def test_transcribe_matches_golden(ctx, case):
+@pytest.mark.parametrize("half", [False, True])
+def test_transcribe_matches_golden(ctx, case, half):
+    """The batch API against transformers' greedy sequences and token timestamps: both timestamp modes (fp32
+    arithmetic, and align.rs's fp16 roundings) give transformers' times on the 20 ms grid."""
     e = case.engine(ctx)
     p = transcribe.Prompt(e.gc, "auto" if case.detect else "en")
-    out, tm = transcribe.transcribe(e, case.mel, p, max_new=case.seq.shape[1] - 4, half_align=False)
+    out, tm = transcribe.transcribe(e, case.mel, p, max_new=case.seq.shape[1] - 4, half_align=half)
     for b, d in enumerate(out):
         if case.detect:
             assert d.lang == int(case.seq[b, 1])

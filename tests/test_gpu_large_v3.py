@@ -6,9 +6,10 @@ Encoder: one clip through the conv stem and all 32 layers with the trace on; the
 checked layer-local (the oracle's layer on the engine's own fp32 input of that layer) at max-abs error <= 2e-3 x RMS.
 
 Decoder: 4 rows teacher-forced on random prompts over random cross keys/values, through all 32 layers in one step:
-at every position every fourth layer layer-local on the engine's residual trace (2e-3 x RMS), the logits against
-the oracle's 32-layer decoder (2e-2 x RMS) and alignment heads spread over layers 16 .. 31 against the oracle's
-probabilities (2e-3 x the largest). Bars as in test_gpu_turbo_widths.py.
+at every position every fourth layer layer-local on the engine's residual trace (2e-3 x RMS), the LM head
+layer-local on the engine's final residual (2e-3 x RMS), the logits against the oracle's 32-layer decoder (2e-2 x
+RMS) and alignment heads spread over layers 16 .. 31 against the oracle's probabilities (2e-3 x the largest). Bars as
+in test_gpu_turbo_widths.py.
 """
 import numpy as np
 import pytest
@@ -31,8 +32,8 @@ def rel_err(got, ref):
 
 
 @pytest.fixture(scope="module")
-def large():
-    W = synth.random_weights(G, seed=8, bias_std=0.02, ln_std=0.1)
+def large(large_v3_weights):
+    W = large_v3_weights
     gen = synth.generation_config(G, align_heads=ALIGN)
     dims = model.Dims(G.d, G.ff, G.nh, G.enc_layers, G.dec_layers, G.n_mels, G.vocab, G.max_t)
     ctx = model.Context(0)
@@ -80,11 +81,15 @@ def test_decoder_large_v3_32_layers(large):
     del xkv
     e.set_trace(True)
     e.reset(prompts)
-    worst = worst_lg = 0.0
+    worst = worst_lg = worst_ll = 0.0
     for pos in range(NP):
         e.step(B, False, NP)
         ref, probs = dec.step(prompts[:, pos].tolist(), pos)
-        worst_lg = max(worst_lg, rel_err(e.logits()[:B], ref))
+        lg = e.logits()[:B]
+        worst_lg = max(worst_lg, rel_err(lg, ref))
+        h = R.layer_norm(e.dec_trace()[-1, :B], Wf["model.decoder.layer_norm.weight"],
+                         Wf["model.decoder.layer_norm.bias"])
+        worst_ll = max(worst_ll, rel_err(lg, R.linear(h, Wf["model.decoder.embed_tokens.weight"])))
         al = e.align()[:B, pos].astype(np.float32)
         for s, (l, h) in enumerate(ALIGN):
             r = probs[:, l, h]
@@ -98,5 +103,7 @@ def test_decoder_large_v3_32_layers(large):
             worst = max(worst, err)
             assert err <= 2e-3, (pos, i, err)
     e.set_trace(False)
-    print("large-v3 decoder, B = 4: layer-local max-abs / RMS", worst, "; logits", worst_lg)
-    assert worst_lg < 2e-2
+    print("large-v3 decoder, B = 4: layer-local max-abs / RMS", worst, "; logits", worst_lg, "; LM head layer-local",
+          worst_ll)
+    assert worst_ll <= 2e-3
+    assert worst_lg < 2e-2  # through all 32 layers from the oracle's own residual stream

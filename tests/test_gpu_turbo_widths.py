@@ -61,18 +61,14 @@ def test_encoder_turbo_widths_layer_local():
         for i in range(g.enc_layers):
             nxt = tr[i + 1, c] if i + 1 < g.enc_layers else xl[c]
             errs.append(rel_err(nxt, R.encoder_layer(tr[i, c], Wf, i, g.nh)))
-        # the final LayerNorm's fp16 output: within one fp16 ulp of the oracle's value (its max-abs error alone is
-        # ~2e-3 x RMS from the rounding of the largest outputs), plus the fp32 evaluation error of the two terms of
-        # (x - mean) rstd w + b in the kernel and in the oracle (4 fp32 ulps of each term's size): near-zero outputs,
-        # where the terms cancel, have fp16 spacings far below that
-        lw = Wf["model.encoder.layer_norm.weight"]
-        lb = Wf["model.encoder.layer_norm.bias"]
-        ref = R.layer_norm(xl[c], lw, lb)
+        # the final LayerNorm's fp16 output within one fp16 ulp of a float64 LayerNorm of the same residual
+        lw = W["model.encoder.layer_norm.weight"].astype(np.float64)
+        lb = W["model.encoder.layer_norm.bias"].astype(np.float64)
         x64 = xl[c].astype(np.float64)
         xc = x64 - x64.mean(-1, keepdims=True)
-        terms = np.abs(xc / np.sqrt((xc ** 2).mean(-1, keepdims=True) + 1e-5) * lw) + np.abs(lb)
-        bound = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) + 2.0 ** -21 * terms
-        excess = np.abs(out[c] - ref) - bound
+        ref = xc / np.sqrt((xc ** 2).mean(-1, keepdims=True) + 1e-5) * lw + lb
+        ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+        excess = np.abs(out[c] - ref) - ulp
         assert np.all(excess <= 0), (np.unravel_index(np.argmax(excess), excess.shape), excess.max())
         print("turbo widths, clip", c, ["%.2e" % x for x in errs])
         assert max(errs) < 2e-3, errs
@@ -96,6 +92,7 @@ def test_decoder_turbo_widths_batch32():
     ctx = model.Context(0)
     e = model.Engine(ctx, dims, gc, B, 8)
     e.load(W)
+    e.set_trace(True)
     p, n = e.buffer(L.BUF_XKV)
     assert n >= xkv.nbytes
     ctx.upload(p, xkv)
@@ -106,12 +103,16 @@ def test_decoder_turbo_widths_batch32():
     e.reset(prompts)
     sup = set(gen["suppress_tokens"])
     bsup = gen["begin_suppress_tokens"]
-    worst, checked = 0.0, 0
+    worst, worst_ll, checked = 0.0, 0.0, 0
     for pos in range(NP):
         e.step(B, False, NP)
         ref, probs = dec.step(prompts[:, pos].tolist(), pos)
         lg = e.logits()[:B]
         worst = max(worst, rel_err(lg, ref))
+        # layer-local: the final LayerNorm and the tied LM head on the engine's own final residual
+        h = R.layer_norm(e.dec_trace()[-1, :B], Wf["model.decoder.layer_norm.weight"],
+                         Wf["model.decoder.layer_norm.bias"])
+        worst_ll = max(worst_ll, rel_err(lg, R.linear(h, Wf["model.decoder.embed_tokens.weight"])))
         al = e.align()[:B, pos].astype(np.float32)  # [B][slots][1500]
         for s, (l, h) in enumerate(gen["alignment_heads"]):
             r = probs[:, l, h]
@@ -123,8 +124,10 @@ def test_decoder_turbo_widths_batch32():
                 if top[1] - top[0] > 1e-2:
                     assert toks[b] == R.choose(ref[b], sup, bsup, True, gen["eos_token_id"], False), b
                     checked += 1
-    print("turbo widths, B = 32: logits max-abs / RMS", worst, "; greedy choices checked", checked)
-    assert worst < 2e-2
+    print("turbo widths, B = 32: logits max-abs / RMS", worst, "; layer-local", worst_ll, "; greedy choices checked",
+          checked)
+    assert worst_ll <= 2e-3
+    assert worst < 2e-2  # through the whole 4-layer decoder from the oracle's own residual stream
     assert checked >= B // 2
     e.close()
     ctx.close()
@@ -133,7 +136,8 @@ def test_decoder_turbo_widths_batch32():
 def test_decoder_turbo_widths_at_position_200():
     """The benchmark's decoder step shape: 32 rows at positions 200 .. 203, the self-attention cache holding 200+
     keys. Every decoder layer layer-local (the oracle's layer on the engine's own residual, cache and cross
-    keys / values) within 2e-3 x RMS, and the logits of the engine's final residual within 2e-2 x RMS."""
+    keys / values) within 2e-3 x RMS, and the logits of the engine's final residual (the final LayerNorm and the tied
+    LM head, layer-local) within 2e-3 x RMS."""
     rng = np.random.default_rng(22)
     W = synth.random_weights(G, seed=6, bias_std=0.02, ln_std=0.1)
     Wf = {k: v.astype(np.float32) for k, v in W.items() if k.startswith("model.decoder")}
@@ -172,6 +176,6 @@ def test_decoder_turbo_widths_at_position_200():
         ref = R.linear(h, Wf["model.decoder.embed_tokens.weight"])
         worst_lg = max(worst_lg, rel_err(e.logits()[:B], ref))
     print("turbo widths, B = 32, positions 200..203: layer-local max-abs / RMS", worst, "; logits", worst_lg)
-    assert worst_lg < 2e-2
+    assert worst_lg <= 2e-3
     e.close()
     ctx.close()
