@@ -219,22 +219,23 @@ def test_graph_replay_bit_identical_at_the_bench_shape(ctx):
         ctx.upload(pd, np.zeros(B, np.int32))
         ctx.upload(pc, np.array([P0, 0, 0, 0], np.int32))
 
-    def outputs():
+    def outputs(i):
+        """What step i (position P0 + i) wrote."""
         kc, vc = e.self_kv()
-        return [e.logits(), e.tokens(), e.done(), kc[:, :, :, P0:P0 + 3].copy(), vc[:, :, :, P0:P0 + 3].copy(),
-                e.align()[:, P0:P0 + 3].copy(), e.dec_x()]
+        return [e.logits(), e.tokens(), e.done(), kc[:, :, :, P0 + i].copy(), vc[:, :, :, P0 + i].copy(),
+                e.align()[:, P0 + i].copy(), e.dec_x()]
 
     start()
     eager = []
-    for _ in range(3):
+    for i in range(3):
         e.step(B, False, 1)
-        eager.append(outputs())
+        eager.append(outputs(i))
     start()
     e.capture(B, 1)
     for i in range(3):
         e.replay()
         ctx.sync()
-        got = outputs()
+        got = outputs(i)
         for k, (a, b) in enumerate(zip(got, eager[i])):
             assert np.array_equal(a, b), (i, k)
     assert e.position() == P0 + 3
