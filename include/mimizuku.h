@@ -242,6 +242,17 @@ int mz_transcribe_device(mz_engine* e, uint64_t mels, const int32_t* frames, int
 int mz_jump_times_device(mz_ctx* c, uint64_t w, int64_t clip_stride, int n, const int32_t* rows, const int32_t* cols,
                          int heads, int cols_full, int width, int half, float* out, int64_t out_stride);
 
+/* mz_jump_times_device without any device allocation: no counterpart in the reference; for callers that cannot
+ * allocate device memory (code under graph capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments and results as mz_jump_times_device (bit for bit). Its scratch is a static 64 MiB array per device
+ * (held until the process ends), located by mz_init; the clips go through it in passes of at most 64 that fit, and a
+ * clip whose own scratch exceeds 64 MiB is refused with MZ_ERR_ARG (e.g. more than about 1,200 rows at 1500 frames).
+ * Every call on a device shares that device's array: calls that overlap on one GPU (other threads, other contexts)
+ * race and must be serialised by the caller. Synchronous on the context's stream. */
+int mz_jump_times_device_noalloc(mz_ctx* c, uint64_t w, int64_t clip_stride, int n, const int32_t* rows,
+                                 const int32_t* cols, int heads, int cols_full, int width, int half, float* out,
+                                 int64_t out_stride);
+
 /* ------------------------------------------------------------------ model directory (host only) */
 
 /* Safetensors file (st::File, src/st.rs:77-181): mapped read-only (read into memory if mapping fails), header

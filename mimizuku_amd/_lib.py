@@ -125,6 +125,7 @@ SIGNATURES = {
     "mz_jump_times": (i32, [P, i32, i32, i32, i32, i32, i32, P]),
     "mz_align_cost": (i32, [P, i32, i32, i32, i32, i32, i32, P]),
     "mz_jump_times_device": (i32, [P, u64, C.c_int64, i32, P, P, i32, i32, i32, i32, P, C.c_int64]),
+    "mz_jump_times_device_noalloc": (i32, [P, u64, C.c_int64, i32, P, P, i32, i32, i32, i32, P, C.c_int64]),
     "mz_dtw": (i32, [P, i32, i32, P, P, P]),
     "mz_f2h": (C.c_uint16, [f32]),
     "mz_h2f": (f32, [C.c_uint16]),

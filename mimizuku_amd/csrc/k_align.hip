@@ -16,7 +16,12 @@
 //                    goes to a trace in the same diagonal-major order, and one lane walks the path back.
 #include <math.h>
 
+#include <algorithm>
+#include <mutex>
+
+#include "../../include/mimizuku.h"
 #include "mz_common.h"
+#include "mz_internal.h"
 #include "mz_kernels.h"
 
 #pragma clang fp contract(off)
@@ -258,4 +263,111 @@ hipError_t mz_ts_launch(hipStream_t s, const MzTs& p, int n) {
     if (mz_ts_lds_bytes(p.ldd - 1) > 64 * 1024 || p.diag_stride * 4 >= (1L << 31)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(ts_dtw_kernel, dim3(n), dim3(nt), mz_ts_lds_bytes(p.ldd - 1), s, p);
     return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ the entry point that allocates nothing
+
+// Scratch of mz_jump_times_device_noalloc: a file-scope device array, one copy per GPU the library runs on, held until
+// the process ends. In host code `scratch` names a host-side stand-in, never a device address: its address on each
+// device comes from hipGetSymbolAddress (mz_ts_scratch_setup, called by mz_init with that device current) and only
+// that address is passed to kernels and copies.
+static __device__ __align__(256) unsigned char scratch[MZ_TS_SCRATCH_BYTES];
+
+namespace {
+constexpr int MZ_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[MZ_MAX_DEVICES] = {};
+size_t up256(size_t n) { return (n + 255) & ~(size_t)255; }
+}  // namespace
+
+int mz_ts_scratch_setup(int device) {
+    if (device < 0 || device >= MZ_MAX_DEVICES) return mz_fail(MZ_ERR_ARG, "device %d: at most %d devices", device, MZ_MAX_DEVICES);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[device]) return MZ_OK;
+    int cur = -1;
+    if (int r = mz_hip(hipGetDevice(&cur), "hipGetDevice")) return r;
+    if (cur != device) return mz_fail(MZ_ERR_STATE, "timestamp scratch set-up: device %d is not current (%d)", device, cur);
+    void* ptr = nullptr;
+    if (int r = mz_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")) return r;
+    if (!ptr) return mz_fail(MZ_ERR_HIP, "hipGetSymbolAddress(scratch) gave a null address");
+    g_scratch[device] = ptr;
+    return MZ_OK;
+}
+
+extern "C" int mz_jump_times_device_noalloc(mz_ctx* c, uint64_t w, int64_t clip_stride, int n, const int32_t* rows,
+                                            const int32_t* cols, int heads, int cols_full, int width, int half,
+                                            float* out, int64_t out_stride) {
+    if (!c || !w || !rows || !cols || !out || n < 0 || heads <= 0 || cols_full <= 0 || clip_stride < 0)
+        return mz_fail(MZ_ERR_ARG, "mz_jump_times_device_noalloc: bad argument");
+    if (width < 1 || width % 2 == 0 || width > MZ_TS_MAX_WIDTH)
+        return mz_fail(MZ_ERR_ARG, "mz_jump_times_device_noalloc: width %d (odd, at most %d)", width, MZ_TS_MAX_WIDTH);
+    for (int i = 0; i < n; i++)
+        if (rows[i] < 0 || cols[i] < 0 || cols[i] > cols_full || rows[i] > 4095 || rows[i] > out_stride)
+            return mz_fail(MZ_ERR_ARG, "mz_jump_times_device_noalloc: clip %d has %d rows, %d columns", i, rows[i],
+                           cols[i]);
+    if (n == 0) return MZ_OK;
+    if (int r = mz_hip(hipSetDevice(c->device), "hipSetDevice")) return r;
+    if (int r = mz_ts_scratch_setup(c->device)) return r;
+    unsigned char* base;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        base = (unsigned char*)g_scratch[c->device];
+    }
+    // scratch of k clips whose longest has rmax rows: (rows, columns), column statistics, DTW cost and trace, times
+    auto need = [&](int k, int rmax) {
+        return up256((size_t)k * sizeof(int2)) + 2 * up256((size_t)k * heads * cols_full * 4) +
+               up256((size_t)k * mz_ts_diag_stride(rmax, cols_full) * 5) + up256((size_t)k * out_stride * 4);
+    };
+    // the clips go through the array in chunks of at most MZ_TS_NOALLOC_CHUNK that fit in it, one after the other
+    int2 rc[MZ_TS_NOALLOC_CHUNK];
+    for (int c0 = 0; c0 < n;) {
+        int k = 0, rmax = 0;
+        while (c0 + k < n && k < MZ_TS_NOALLOC_CHUNK && need(k + 1, std::max(rmax, (int)rows[c0 + k])) <= MZ_TS_SCRATCH_BYTES) {
+            rmax = std::max(rmax, (int)rows[c0 + k]);
+            k++;
+        }
+        if (k == 0)
+            return mz_fail(MZ_ERR_ARG,
+                           "mz_jump_times_device_noalloc: clip %d (%d rows, %d heads x %d columns) needs %zu bytes of "
+                           "scratch; the static scratch holds %u",
+                           c0, rows[c0], heads, cols_full, need(1, rows[c0]), (unsigned)MZ_TS_SCRATCH_BYTES);
+        for (int i = 0; i < k; i++) rc[i] = int2{rows[c0 + i], cols[c0 + i]};
+        const long ds = mz_ts_diag_stride(rmax, cols_full);
+        unsigned char* q = base;
+        auto carve = [&](size_t bytes) {
+            unsigned char* r = q;
+            q += up256(bytes);
+            return r;
+        };
+        MzTs p{};
+        p.w = (const float*)(uintptr_t)w + (size_t)c0 * clip_stride;
+        p.clip_stride = clip_stride;
+        p.heads = heads;
+        p.cols_full = cols_full;
+        p.width = width;
+        p.half = half;
+        p.rmax = rmax;
+        p.rc = (const int2*)carve((size_t)k * sizeof(int2));
+        p.mean = (float*)carve((size_t)k * heads * cols_full * 4);
+        p.sd = (float*)carve((size_t)k * heads * cols_full * 4);
+        p.cost = (float*)carve((size_t)k * ds * 5);
+        p.trace = (signed char*)(p.cost + (size_t)k * ds);
+        p.diag_stride = ds;
+        p.ldd = rmax + 1;
+        p.out = (float*)carve((size_t)k * out_stride * 4);
+        p.out_stride = out_stride;
+        int r = mz_hip(hipMemcpyAsync((void*)p.rc, rc, (size_t)k * sizeof(int2), hipMemcpyHostToDevice, c->stream),
+                       "upload");
+        if (!r) r = mz_hip(mz_ts_launch(c->stream, p, k), "timestamp kernels");
+        for (int i = 0; i < k && !r; i++)
+            if (rows[c0 + i] > 0)
+                r = mz_hip(hipMemcpyAsync(out + (size_t)(c0 + i) * out_stride, p.out + (size_t)i * out_stride,
+                                          (size_t)rows[c0 + i] * 4, hipMemcpyDeviceToHost, c->stream),
+                           "download");
+        // the next chunk reuses the array (and rc): wait for this one
+        if (!r) r = mz_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        if (r) return r;
+        c0 += k;
+    }
+    return MZ_OK;
 }

@@ -151,6 +151,11 @@ struct MzTs {
 // scratch elements per clip for cost / trace
 inline long mz_ts_diag_stride(int rmax, int cols_full) { return (long)(rmax + cols_full + 1) * (rmax + 1); }
 hipError_t mz_ts_launch(hipStream_t s, const MzTs& p, int n);
+// the static scratch of mz_jump_times_device_noalloc (64 MiB per device) and the clips it takes per pass
+#define MZ_TS_SCRATCH_BYTES (64u << 20)
+#define MZ_TS_NOALLOC_CHUNK 64
+// looks up that scratch's address on `device` (which must be current) once; mz_init calls it
+int mz_ts_scratch_setup(int device);
 
 // ---------------------------------------------------------------- log-mel features (Mel::features, src/audio.rs)
 #define MZ_MEL_NFFT 400

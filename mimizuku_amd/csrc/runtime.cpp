@@ -46,6 +46,8 @@ extern "C" int mz_init(int device, mz_ctx** out) {
     if (e != hipSuccess || n <= 0) return mz_fail(MZ_ERR_HIP, "mz_init: no HIP device available (%s)", hipGetErrorString(e));
     if (device < 0 || device >= n) return mz_fail(MZ_ERR_ARG, "mz_init: device %d of %d", device, n);
     if (int r = mz_hip(hipSetDevice(device), "hipSetDevice")) return r;
+    // the no-allocation timestamp entry point's static scratch: its address on this device, looked up once
+    if (int r = mz_ts_scratch_setup(device)) return r;
     auto* c = new mz_ctx();
     c->device = device;
     // graph capture is not allowed on the legacy default stream (src/gpu.rs:125); default priority

@@ -129,6 +129,20 @@ def jump_times_device(ctx, w: int, clip_stride: int, rows, cols, heads: int, col
     return [out[c, :rows[c]] for c in range(n)]
 
 
+def jump_times_device_noalloc(ctx, w: int, clip_stride: int, rows, cols, heads: int, cols_full: int, width: int = 7,
+                              half: bool = True) -> list[np.ndarray]:
+    """jump_times_device through the entry point that allocates no device memory (its scratch is a static array per
+    device): the same times, bit for bit."""
+    rows = np.ascontiguousarray(rows, np.int32)
+    cols = np.ascontiguousarray(cols, np.int32)
+    n = len(rows)
+    stride = max(int(rows.max()) if n else 0, 1)
+    out = np.zeros((n, stride), np.float32)
+    check(L.lib().mz_jump_times_device_noalloc(ctx.h, w, clip_stride, n, ptr(rows), ptr(cols), heads, cols_full,
+                                               width, int(half), ptr(out), stride))
+    return [out[c, :rows[c]] for c in range(n)]
+
+
 def dtw(m: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """DTW path (text, time indices) over cost m [rows][cols] (src/align.rs:66-106)."""
     m = np.ascontiguousarray(m, np.float64)
