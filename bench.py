@@ -5,17 +5,17 @@
 One step = one pass of the batch transcription API over 32 synthetic 30 s clips with large-v3-turbo geometry and
 seeded random-init fp16 weights: the encoder in groups of 8 clips (conv stem, 32 layers, every decoder layer's cross
 k/v), language detection, greedy decoding of up to 224 tokens by replaying one captured step graph, and token
-timestamps from the alignment heads (median filter + DTW on the host). The log-mel inputs are resident in device
+timestamps from the alignment heads (median filter + DTW on the device). The log-mel inputs are resident in device
 memory before the timed region. Prints one JSON line: audio-seconds per second (value), with the encoder TFLOP/s, the
-decoder step time, per-kernel event timings, the roofline of the dominant kernel and the CPU oracle on a bounded
-sample of the same workload.
+decoder step time, per-kernel event timings of the encoder and decoder kernels ranked by their time per headline
+step, the roofline of the dominant kernel, the same workload on the full large-v3 geometry (32 + 32 layers), and the
+CPU baseline (a torch restatement of the oracle, in a child process) per benchmark configuration.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
-import platform
 import sys
 import time
 
@@ -53,6 +53,27 @@ def kernel_work(g, G: int) -> dict:
     }
 
 
+def dec_kernel_bytes(g, B: int, p: int, na: int) -> dict:
+    """Algorithmic HBM bytes of one launch of each decoder kernel class at position p for B rows (weights and cross
+    keys/values read once, activations read and written once; split-K partials in fp32)."""
+    d, ff, nl, V = g.d, g.ff, g.dec_layers, g.vocab
+    ks_dd, ks_df = 5, 5  # split-K slices of the out-projections (K = 1280) and fc2 (K = 5120)
+    act = B * d * 2
+    return {
+        "dec_embed": B * d * (2 + 2 + 4 + 2),
+        "dec_qkv": 3 * d * d * 2 + act + B * d * 4 + 2 * act,
+        "dec_self": B * 2 * (p + 1) * d * 2 + B * d * 4 + act,
+        "dec_oproj": d * d * 2 + act + ks_dd * B * d * 4,
+        "dec_addln": B * d * 4 * (ks_dd + 2) + act,
+        "dec_cross": B * 2 * 1500 * d * 2 + d * d * 2 + 2 * act + B * (na / nl) * 1500 * 4,
+        "dec_xo": d * d * 2 + act + ks_dd * B * d * 4,
+        "dec_fc1": ff * d * 2 + act + B * ff * 2,
+        "dec_fc2": d * ff * 2 + B * ff * 2 + ks_df * B * d * 4,
+        "dec_lm": V * d * 2 + B * V * 4 + act,
+        "dec_argmax": B * 8 * ((V + 207) // 208) + B * 4,
+    }
+
+
 def encoder_flops(g, n: int) -> float:
     w = kernel_work(g, 1)
     per_clip = w["conv1"][1] + w["conv2"][1] + w["xkv"][1] + g.enc_layers * sum(
@@ -71,47 +92,21 @@ def decode_step_bytes(g, B: int, p: int, na: int) -> float:
     return cross + weights + head + selfkv + B * V * 4 + B * na * 1500 * 2
 
 
-def cpu_baseline(g, W16: dict, gen: dict, mel: np.ndarray, steps: int) -> dict:
-    """The oracle (fp32 numpy) on a bounded sample: the conv stem, one encoder layer and the cross k/v of one clip,
-    and two decoder steps of the 32-row batch; extrapolated to the whole workload (32 clips x 32 layers, `steps`
-    decoder steps)."""
-    from oracle import whisper_ref as R
+def cpu_baseline(steps: int, timeout: int = 900) -> dict | None:
+    """The CPU baseline in a child process (oracle/cpu_torch.py: an fp32 torch restatement of the oracle, timed per
+    benchmark configuration on the host's CPU share), so torch is never loaded into the process that drives the GPU."""
+    import subprocess
+    env = dict(os.environ, HIP_VISIBLE_DEVICES="", CUDA_VISIBLE_DEVICES="", ROCR_VISIBLE_DEVICES="")
     try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-    except Exception:  # pragma: no cover
-        threads = os.cpu_count() or 1
-    keep = [k for k in W16 if not k.startswith("model.encoder.layers.") or k.startswith("model.encoder.layers.0.")]
-    W = {k: W16[k].astype(np.float32) for k in keep}
-
-    def med(f, n=3):
-        ts = []
-        for _ in range(n):
-            t = time.perf_counter()
-            f()
-            ts.append(time.perf_counter() - t)
-        return float(np.median(ts)), ts
-
-    m0 = mel[0].astype(np.float32)
-    t_stem, _ = med(lambda: R.conv_stem(m0, W))
-    x = R.conv_stem(m0, W)
-    t_layer, _ = med(lambda: R.encoder_layer(x, W, 0, g.nh))
-    t_xkv, _ = med(lambda: R.cross_kv(x, W, g.dec_layers, g.nh))
-    xkv = R.cross_kv(x, W, g.dec_layers, g.nh)
-    dec = R.Decoder(W, g.nh, g.dec_layers, [xkv] * N_CLIPS)
-    toks = [gen["decoder_start_token_id"]] * N_CLIPS
-    t0 = time.perf_counter()
-    for p in range(2):
-        dec.step(toks, p)
-    t_step = (time.perf_counter() - t0) / 2
-    enc = N_CLIPS * (t_stem + g.enc_layers * t_layer + t_xkv)
-    total = enc + steps * t_step
-    return {"value": N_CLIPS * 30.0 / total, "unit": "audio-sec/sec", "cores": int(threads), "kind": "port",
-            "sample": (f"oracle fp32 numpy on {threads} BLAS threads ({os.cpu_count()} host cpus, "
-                       f"{platform.processor() or platform.machine()}): conv stem {t_stem:.3f}s, one encoder layer "
-                       f"{t_layer:.3f}s and cross k/v {t_xkv:.3f}s of one clip (median of 3), decoder step at "
-                       f"B=32 {t_step:.3f}s (mean of 2); extrapolated to 32 clips x {g.enc_layers} layers + "
-                       f"{steps} steps = {total:.1f}s")}
+        r = subprocess.run([sys.executable, "-m", "oracle.cpu_torch", "--steps", str(steps)], cwd=ROOT, env=env,
+                           capture_output=True, text=True, timeout=timeout)
+    except subprocess.TimeoutExpired:
+        log("bench: CPU baseline timed out")
+        return None
+    if r.returncode != 0:
+        log(f"bench: CPU baseline failed: {r.stderr[-500:]}")
+        return None
+    return json.loads(r.stdout.strip().splitlines()[-1])
 
 
 def probe(name: str, reps: int = 5):
@@ -128,6 +123,31 @@ def probe(name: str, reps: int = 5):
     def f16(shape, sc=1.0):
         return (rng.standard_normal(shape, dtype=np.float32) * sc).astype(np.float16)
 
+    if name == "dec_step":
+        # three eager turbo decoder steps at B = 32 from position 200 (random self cache and cross keys/values):
+        # the decoder kernels at the benchmark's step shape, one dispatch each per layer and step
+        gd = synth.Geometry(d=d, ff=ff, nh=nh, enc_layers=1, dec_layers=g.dec_layers, n_mels=g.n_mels, vocab=g.vocab)
+        W = synth.random_weights(gd, seed=0)
+        gen = synth.generation_config(gd, align_heads=synth.generation_config(g)["alignment_heads"])
+        dims = model.Dims(gd.d, gd.ff, gd.nh, gd.enc_layers, gd.dec_layers, gd.n_mels, gd.vocab, gd.max_t)
+        e = model.Engine(ctx, dims, model.GenCfg.from_dict(gen, dims), N_CLIPS, EG)
+        e.load(W)
+        for which, shape in ((L.BUF_XKV, (N_CLIPS, gd.dec_layers, 2, nh, 1536, 64)),
+                             (L.BUF_SELF_K, (gd.dec_layers, N_CLIPS, nh, gd.max_t, 64)),
+                             (L.BUF_SELF_V, (gd.dec_layers, N_CLIPS, nh, gd.max_t, 64))):
+            p, _ = e.buffer(which)
+            ctx.upload(p, f16(shape))
+        toks = rng.integers(0, 50000, size=(N_CLIPS, gd.max_t)).astype(np.int32)
+        e.reset(toks[:, :1])
+        ctx.upload(e.buffer(L.BUF_TOK)[0], toks)
+        ctx.upload(e.buffer(L.BUF_CTR)[0], np.array([200, 0, 0, 0], np.int32))
+        for _ in range(3):
+            e.step(N_CLIPS, False, 1)
+        ctx.sync()
+        print(json.dumps({"probe": name, "steps": 3, "position": 200,
+                          "dec_cross_bytes": dec_kernel_bytes(g, N_CLIPS, 201, 6)["dec_cross"]}))
+        e.close()
+        return
     if name == "copy":
         nbytes = 512 << 20
         a, b = ctx.alloc(nbytes), ctx.alloc(nbytes)
@@ -177,17 +197,153 @@ def probe(name: str, reps: int = 5):
     print(json.dumps({"probe": name, "launches": reps, "algorithmic": amount, "bound": bound}))
 
 
+def run_model(g, seed: int, steps: int, warmup: int, graph: bool, label: str, L, model, synth, transcribe):
+    """The headline workload on geometry g: an engine for 32 rows and groups of 8, the timed transcription steps, then
+    (outside the timed region) the encoder kernels timed per launch, the decoder step at B = 32, p = 200..219 by graph
+    replay, and the decoder kernels timed per launch in eager steps. Returns the engine's context objects and the
+    measurements."""
+    log(f"bench: drawing {label} weights (seed {seed}) and {N_CLIPS} log-mel clips")
+    W = synth.random_weights(g, seed=seed)
+    gen = synth.generation_config(g)
+    mel = synth.synthetic_mel(N_CLIPS, g.n_mels, seed=1)
+    dims = model.Dims(g.d, g.ff, g.nh, g.enc_layers, g.dec_layers, g.n_mels, g.vocab, g.max_t)
+    gc = model.GenCfg.from_dict(gen, dims)
+    ctx = model.Context(0)
+    e = model.Engine(ctx, dims, gc, N_CLIPS, EG)
+    e.load(W)
+    del W
+    dmel = ctx.upload_new(mel)
+    prompt = transcribe.Prompt(gc, "auto", "transcribe")
+    log(f"bench: {label} engine ready")
+
+    def step():
+        return transcribe.transcribe(e, dmel, prompt, max_new=MAX_NEW, n=N_CLIPS, graph=graph)
+
+    for i in range(warmup):
+        out, tm = step()
+        log(f"bench: {label} warmup {i}: enc {tm.enc * 1e3:.1f} ms, dec {tm.dec * 1e3:.1f} ms ({tm.steps} steps), "
+            f"post {tm.post * 1e3:.1f} ms")
+    ctx.sync()
+    t0 = time.perf_counter()
+    tms = []
+    for i in range(steps):
+        out, tm = step()
+        tms.append(tm)
+    ctx.sync()
+    dt = time.perf_counter() - t0
+    r = {"dt": dt, "ms_step": dt / steps * 1e3, "value": N_CLIPS * 30.0 / (dt / steps),
+         "enc_s": float(np.mean([t.enc for t in tms])), "dec_s": float(np.mean([t.dec for t in tms])),
+         "post_s": float(np.mean([t.post for t in tms])), "nsteps": tms[-1].steps, "na": len(gen["alignment_heads"])}
+    log(f"bench: {label}: {steps} steps in {dt:.3f}s = {r['ms_step']:.1f} ms/step, {r['value']:.0f} audio-s/s")
+
+    # encoder kernels, HIP events around every launch: the transcription overlaps two encoder groups on two streams,
+    # so each kernel class is timed in one more encoder pass over the same clips with the groups one after the other
+    e.profile(True)
+    for g0 in range(0, N_CLIPS, EG):
+        e.encode_device(dmel + g0 * g.n_mels * 3000 * 4, min(EG, N_CLIPS - g0), g0)
+    ctx.sync()
+    r["enc_prof"] = e.profile_read()
+    e.profile(False)
+
+    # the decoder step alone at the 32-row batch, positions 200..219 (self-attention cache of 201..220 entries)
+    rng = np.random.default_rng(7)
+    nprompt = 200
+    pr = rng.integers(0, 50000, size=(N_CLIPS, nprompt)).astype(np.int32)
+    e.reset(pr)
+    if graph:
+        e.capture(N_CLIPS, nprompt)
+        for _ in range(200):
+            e.replay()
+        ctx.sync()
+        e.profile(True)
+        for _ in range(20):
+            e.replay()
+        st_ms, st_n = e.profile_read()["step"]
+        e.profile(False)
+        r["step_us"] = st_ms / st_n * 1e3
+    else:
+        for _ in range(200):
+            e.step(N_CLIPS, False, nprompt)
+        ctx.sync()
+        ev0, ev1 = ctx.event(), ctx.event()
+        ctx.record(ev0)
+        for _ in range(20):
+            e.step(N_CLIPS, False, nprompt)
+        ctx.record(ev1)
+        r["step_us"] = ctx.elapsed_ms(ev0, ev1) / 20 * 1e3
+    r["step_bytes"] = float(np.mean([decode_step_bytes(g, N_CLIPS, p, r["na"]) for p in range(200, 220)]))
+    log(f"bench: {label} decode step at B=32, p=200..219: {r['step_us']:.1f} us, "
+        f"{r['step_bytes'] / (r['step_us'] * 1e-6) / 1e9:.0f} GB/s")
+    # decoder kernels, HIP events around every launch of three eager steps (p = 220..222)
+    e.profile(True)
+    for _ in range(3):
+        e.step(N_CLIPS, False, nprompt)
+    ctx.sync()
+    r["dec_prof"] = {k: v for k, v in e.profile_read().items() if k.startswith("dec_")}
+    e.profile(False)
+    return ctx, e, dmel, r
+
+
+def kernel_table(g, r) -> dict:
+    """Per kernel class: launches, average event time, throughput against its roofline, and its time per headline
+    step (encoder classes: the launches of one 32-clip encoder pass; decoder classes: launches per step x the decode
+    steps of a headline step)."""
+    work = kernel_work(g, EG)
+    dbytes = dec_kernel_bytes(g, N_CLIPS, 221, r["na"])
+    steps = 3
+    out = {}
+    for name, (ms, n) in list(r["enc_prof"].items()) + list(r["dec_prof"].items()):
+        if not n or name == "step":
+            continue
+        avg = ms / n * 1e-3
+        if name.startswith("dec_"):
+            bound, amount = "hbm", dbytes[name]
+            per_step = ms / steps * r["nsteps"]
+        else:
+            bound, amount = work[name]
+            per_step = ms
+        peak = PEAK_F16 if bound == "mfma" else PEAK_HBM
+        out[name] = {"launches": n, "avg_us": round(avg * 1e6, 2), "bound": bound,
+                     ("tflops" if bound == "mfma" else "gbps"): round(amount / avg / (1e12 if bound == "mfma" else 1e9), 2),
+                     "frac": round(amount / avg / peak, 4), "ms_per_headline_step": round(per_step, 3)}
+    return out
+
+
+def roofline(g, r, kernels: dict, name: str) -> dict:
+    k = kernels[name]
+    if name.startswith("dec_"):
+        bound, amount = "hbm", dec_kernel_bytes(g, N_CLIPS, 221, r["na"])[name]
+        unit = f"{amount / 1e6:.1f} MB (32 rows at position ~221)"
+    else:
+        bound, amount = kernel_work(g, EG)[name]
+        unit = f"{amount / 1e9:.2f} G{'FLOP' if bound == 'mfma' else 'B'} ({EG} clips x 1500 frames)"
+    avg = k["avg_us"] * 1e-6
+    traffic = traffic_src = None
+    tf = os.path.join(ROOT, "profiles", "traffic.json")  # HBM bytes per launch from rocprofv3 FETCH/WRITE_SIZE runs
+    if os.path.exists(tf):
+        with open(tf) as f:
+            t = json.load(f).get(name)
+        if t:
+            traffic, traffic_src = t["bytes_per_launch"], t["source"]
+    return {"kernel": name, "bound": bound, "achieved": round(amount / avg / (1e12 if bound == "mfma" else 1e9), 2),
+            "peak": 2500.0 if bound == "mfma" else 8000.0, "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
+            "frac": k["frac"], "traffic": traffic, "traffic_source": traffic_src, "per_launch": unit,
+            "ms_per_headline_step": k["ms_per_headline_step"]}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-large", action="store_true", help="skip the large-v3 (32 + 32 layers) measurement")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch every decoder step's kernels instead of replaying the captured graph (as the "
                          "reference's --no-graph; for kernel tracers that do not follow graph launches)")
     ap.add_argument("--probe", default=None,
-                    help="run one kernel class at the bench shape (or 'copy') for counter runs, then exit")
+                    help="run one kernel class at the bench shape, the decoder step ('dec_step') or a copy ('copy') "
+                         "for counter runs, then exit")
     a = ap.parse_args()
     if a.probe:
         probe(a.probe)
@@ -203,108 +359,13 @@ def main():
     from mimizuku_amd import model, synth, transcribe
 
     g = synth.LARGE_V3_TURBO
-    log(f"bench: drawing large-v3-turbo weights (seed 0) and {N_CLIPS} log-mel clips")
-    W = synth.random_weights(g, seed=0)
-    gen = synth.generation_config(g)
-    mel = synth.synthetic_mel(N_CLIPS, g.n_mels, seed=1)
-    dims = model.Dims(g.d, g.ff, g.nh, g.enc_layers, g.dec_layers, g.n_mels, g.vocab, g.max_t)
-    gc = model.GenCfg.from_dict(gen, dims)
-    ctx = model.Context(0)
-    e = model.Engine(ctx, dims, gc, N_CLIPS, EG)
-    e.load(W)
-    dmel = ctx.upload_new(mel)
-    prompt = transcribe.Prompt(gc, "auto", "transcribe")
-    log("bench: engine ready")
-
-    def step():
-        return transcribe.transcribe(e, dmel, prompt, max_new=MAX_NEW, n=N_CLIPS, graph=not a.no_graph)
-
-    for i in range(a.warmup):
-        out, tm = step()
-        log(f"bench: warmup {i}: enc {tm.enc * 1e3:.1f} ms, dec {tm.dec * 1e3:.1f} ms ({tm.steps} steps), "
-            f"post {tm.post * 1e3:.1f} ms")
-    ctx.sync()
-    t0 = time.perf_counter()
-    tms = []
-    for i in range(a.steps):
-        out, tm = step()
-        tms.append(tm)
-    ctx.sync()
-    dt = time.perf_counter() - t0
-    ms_step = dt / a.steps * 1e3
-    value = N_CLIPS * 30.0 / (dt / a.steps)
-    enc_s = float(np.mean([t.enc for t in tms]))
-    dec_s = float(np.mean([t.dec for t in tms]))
-    post_s = float(np.mean([t.post for t in tms]))
-    nsteps = tms[-1].steps
-    log(f"bench: {a.steps} steps in {dt:.3f}s = {ms_step:.1f} ms/step, {value:.0f} audio-s/s")
-
-    # Per-kernel timings: the transcription overlaps two encoder groups on two streams, so its launches share the GPU;
-    # each kernel class is timed instead in one more encoder pass over the same clips with the groups one after the
-    # other on the engine's stream (HIP events around every launch).
-    e.profile(True)
-    for g0 in range(0, N_CLIPS, EG):
-        e.encode_device(dmel + g0 * g.n_mels * 3000 * 4, min(EG, N_CLIPS - g0), g0)
-    ctx.sync()
-    prof = e.profile_read()
-    e.profile(False)
-    work = kernel_work(g, EG)
-    kernels = {}
-    for name, (ms, n) in prof.items():
-        if not n or name == "step":
-            continue
-        avg = ms / n * 1e-3
-        bound, amount = work[name]
-        peak = PEAK_F16 if bound == "mfma" else PEAK_HBM
-        kernels[name] = {"launches": n, "avg_us": round(avg * 1e6, 2), "total_ms": round(ms, 3), "bound": bound,
-                         ("tflops" if bound == "mfma" else "gbps"): round(amount / avg / (1e12 if bound == "mfma" else 1e9), 2),
-                         "frac": round(amount / avg / peak, 4)}
-    dom = max(kernels, key=lambda k: kernels[k]["total_ms"])
-    dk = kernels[dom]
-    bound, amount = work[dom]
-    avg = dk["avg_us"] * 1e-6
-    traffic, traffic_src = None, None
-    tf = os.path.join(ROOT, "profiles", "traffic.json")  # HBM bytes per launch from rocprofv3 FETCH/WRITE_SIZE runs
-    if os.path.exists(tf):
-        with open(tf) as f:
-            t = json.load(f).get(dom)
-        if t:
-            traffic, traffic_src = t["bytes_per_launch"], t["source"]
-    roof = {"kernel": dom, "bound": bound, "achieved": round(amount / avg / (1e12 if bound == "mfma" else 1e9), 2),
-            "peak": 2500.0 if bound == "mfma" else 8000.0, "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
-            "frac": dk["frac"], "traffic": traffic, "traffic_source": traffic_src,
-            "per_launch": f"{amount / 1e9:.2f} G{'FLOP' if bound == 'mfma' else 'B'} ({EG} clips x 1500 frames)"}
-
-    # decoder step alone at the 32-row batch, positions 200..219 (self-attention cache of 201..220 entries)
-    rng = np.random.default_rng(7)
-    nprompt = 200
-    pr = rng.integers(0, 50000, size=(N_CLIPS, nprompt)).astype(np.int32)
-    e.reset(pr)
-    if a.no_graph:
-        for _ in range(200):
-            e.step(N_CLIPS, False, nprompt)
-        ctx.sync()
-        ev0, ev1 = ctx.event(), ctx.event()
-        ctx.record(ev0)
-        for _ in range(20):
-            e.step(N_CLIPS, False, nprompt)
-        ctx.record(ev1)
-        step_us = ctx.elapsed_ms(ev0, ev1) / 20 * 1e3
-    else:
-        e.capture(N_CLIPS, nprompt)
-        for _ in range(200):
-            e.replay()
-        ctx.sync()
-        e.profile(True)
-        for _ in range(20):
-            e.replay()
-        st_ms, st_n = e.profile_read()["step"]
-        e.profile(False)
-        step_us = st_ms / st_n * 1e3
-    na = len(gen["alignment_heads"])
-    step_bytes = float(np.mean([decode_step_bytes(g, N_CLIPS, p, na) for p in range(200, 220)]))
-    log(f"bench: decode step at B=32, p=200..219: {step_us:.1f} us, "
-        f"{step_bytes / (step_us * 1e-6) / 1e9:.0f} GB/s")
+    ctx, e, dmel, r = run_model(g, 0, a.steps, a.warmup, not a.no_graph, "large-v3-turbo", L, model, synth, transcribe)
+    kernels = kernel_table(g, r)
+    ranked = sorted(kernels, key=lambda k: -kernels[k]["ms_per_headline_step"])
+    roof = roofline(g, r, kernels, ranked[0])
+    second = next(k for k in ranked if not k.startswith("dec_"))  # the largest encoder class, for the record
+    log("bench: kernel classes by time per headline step: " +
+        ", ".join(f"{k} {kernels[k]['ms_per_headline_step']:.1f} ms" for k in ranked[:6]))
 
     # off the metric: the log-mel front end on the device for the same 32 clips as 30 s of 16 kHz audio
     rng = np.random.default_rng(3)
@@ -320,37 +381,79 @@ def main():
     ctx.free(d_audio)
     ctx.free(d_feat)
     log(f"bench: log-mel of {N_CLIPS} x 30 s on the device: {min(fms):.2f} ms")
+    e.close()
+    ctx.close()
+
+    large = None
+    if not a.no_large:
+        gl = synth.LARGE_V3
+        ctx2, e2, _, rl = run_model(gl, 0, 2, 1, not a.no_graph, "large-v3", L, model, synth, transcribe)
+        kl = kernel_table(gl, rl)
+        large = {"value": round(rl["value"], 2), "unit": "audio-sec/sec", "ms_per_step": round(rl["ms_step"], 3),
+                 "steps": 2, "warmup": 1,
+                 "encoder_tflops": round(encoder_flops(gl, N_CLIPS) / rl["enc_s"] / 1e12, 2),
+                 "encoder_ms": round(rl["enc_s"] * 1e3, 3), "decode_ms": round(rl["dec_s"] * 1e3, 3),
+                 "post_ms": round(rl["post_s"] * 1e3, 3), "decode_steps": rl["nsteps"],
+                 "decode_step_us": round(rl["step_us"], 2),
+                 "decode_step_hbm_frac": round(rl["step_bytes"] / (rl["step_us"] * 1e-6) / PEAK_HBM, 4),
+                 "dec_cross": kl.get("dec_cross"),
+                 "config": "large-v3 (32 encoder + 32 decoder layers, d 1280, 128 mels), 32 clips x 30 s, groups of "
+                           "8, language detection, greedy <= 224 tokens (graph replay), token timestamps"}
+        e2.close()
+        ctx2.close()
 
     res = {
-        "metric": METRIC, "value": round(value, 2), "unit": "audio-sec/sec", "n_gpus": 1, "steps": a.steps,
-        "warmup": a.warmup, "ms_per_step": round(ms_step, 3), "higher_is_better": True, "scaling": "weak",
+        "metric": METRIC, "value": round(r["value"], 2), "unit": "audio-sec/sec", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(r["ms_step"], 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f16",
         "data": "synthetic log-mel N(-0.3,0.4) clamped, seeded random-init weights (no checkpoint)",
         "config": {"workload": "large-v3-turbo end to end: 32 clips x 30 s, encoder groups of 8 (two at a time on two "
                                "streams), language detection, greedy <= 224 tokens (graph replay), token timestamps",
-                   "batch": N_CLIPS, "enc_group": EG, "max_new_tokens": MAX_NEW, "decode_steps": nsteps,
+                   "batch": N_CLIPS, "enc_group": EG, "max_new_tokens": MAX_NEW, "decode_steps": r["nsteps"],
                    "graph": not a.no_graph},
-        "encoder_tflops": round(encoder_flops(g, N_CLIPS) / enc_s / 1e12, 2),
-        "encoder_ms": round(enc_s * 1e3, 3), "decode_ms": round(dec_s * 1e3, 3), "post_ms": round(post_s * 1e3, 3),
-        "decode_step_us": round(step_us, 2),
-        "decode_step_hbm_frac": round(step_bytes / (step_us * 1e-6) / PEAK_HBM, 4),
-        "decode_step_us_e2e_avg": round(dec_s / nsteps * 1e6, 2),
+        "encoder_tflops": round(encoder_flops(g, N_CLIPS) / r["enc_s"] / 1e12, 2),
+        "encoder_ms": round(r["enc_s"] * 1e3, 3), "decode_ms": round(r["dec_s"] * 1e3, 3),
+        "post_ms": round(r["post_s"] * 1e3, 3),
+        "decode_step_us": round(r["step_us"], 2),
+        "decode_step_hbm_frac": round(r["step_bytes"] / (r["step_us"] * 1e-6) / PEAK_HBM, 4),
+        "decode_step_us_e2e_avg": round(r["dec_s"] / r["nsteps"] * 1e6, 2),
         "kernels": kernels,
-        "kernel_timing": "HIP events around every launch of one extra encoder pass over the 32 clips with the groups "
-                         "one after the other on one stream (the timed steps overlap two groups)",
+        "kernel_timing": "HIP events around every launch: the encoder classes in one extra encoder pass over the 32 "
+                         "clips with the groups one after the other on one stream (the timed steps overlap two "
+                         "groups), the decoder classes in three eager steps at B = 32, p = 220..222; ranked by time "
+                         "per headline step (encoder: one 32-clip pass; decoder: launches per step x decode steps)",
         "roofline": roof,
+        "roofline_encoder": roofline(g, r, kernels, second),
+        "large_v3": large,
         "features": {"clips": N_CLIPS, "ms": round(min(fms), 3),
                      "scope": "off the metric (the workload feeds log-mel): mz_log_mel over 32 x 30 s of 16 kHz audio "
                               "already in device memory, wall time of the synchronous call (tables, scratch, three "
                               "kernels), best of 3"},
     }
-    if not a.no_cpu:
-        log("bench: CPU oracle sample")
-        res["cpu_baseline"] = cpu_baseline(g, W, gen, mel, nsteps)
+    # the benchmark configurations on the GPU (kernel times from the table above)
+    layer_kernels = ("qkv", "attn", "oproj", "fc1", "fc2")
+    layer_us = sum(kernels[k]["avg_us"] for k in layer_kernels) + 2 * kernels["ln"]["avg_us"]
+    res["configs"] = {
+        "2_attention_us": kernels["attn"]["avg_us"],
+        "3_layer_us": round(layer_us, 2),
+        "3_layer_tflops": round(564.0e9 / (layer_us * 1e-6) / 1e12, 2),
+        "4_decode_step_us": round(r["step_us"], 2),
+    }
+    cpu = None if a.no_cpu else (log("bench: CPU baseline (torch, child process)") or cpu_baseline(r["nsteps"]))
+    if cpu:
+        res["cpu_baseline"] = {
+            "value": round(cpu["config5_audio_s_per_s"], 3), "unit": "audio-sec/sec", "cores": cpu["threads"],
+            "kind": "port",
+            "sample": (f"fp32 torch restatement of the oracle (oracle/cpu_torch.py) on {cpu['threads']} threads "
+                       f"({cpu['host_cpus']} host cpus, {cpu['cpu']}); {cpu['config5_note']}: "
+                       f"{cpu['config5_total_s']:.1f} s"),
+            "configs": {"2_attention_s": round(cpu["config2_attention_s"], 4),
+                        "3_layer_s": round(cpu["config3_layer_s"], 4),
+                        "4_decode_step_s": round(cpu["config4_step_s"], 4),
+                        "stem_8_clips_s": round(cpu["stem_s"], 4), "cross_kv_8_clips_s": round(cpu["cross_kv_s"], 4)},
+        }
     else:
         res["cpu_baseline"] = None
-    e.close()
-    ctx.close()
     print(json.dumps(res), flush=True)
 
 

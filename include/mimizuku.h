@@ -177,8 +177,9 @@ int mz_engine_replay(mz_engine* e);
 int mz_engine_set_trace(mz_engine* e, int on);
 
 /* Kernel timing (the reference's stage timings, src/main.rs:213-222, at kernel granularity): with profiling on, every
- * encoder launch and every graph replay is bracketed by events on the engine's stream. mz_engine_profile clears the
- * records; mz_engine_profile_read sums the elapsed time and counts the launches of one kernel class. */
+ * encoder launch, every kernel of an eager decoder step and every graph replay is bracketed by events on the
+ * engine's stream. mz_engine_profile clears the records; mz_engine_profile_read sums the elapsed time and counts the
+ * launches of one kernel class. */
 #define MZ_K_MEL 0   /* log-mel layout change */
 #define MZ_K_CONV1 1 /* conv1 + GELU (implicit GEMM) */
 #define MZ_K_CONV2 2 /* conv2 + GELU + positions */
@@ -190,6 +191,17 @@ int mz_engine_set_trace(mz_engine* e, int on);
 #define MZ_K_FC2 8   /* fc2 + residual */
 #define MZ_K_XKV 9   /* every decoder layer's cross k/v */
 #define MZ_K_STEP 10 /* one replay of the captured decoder step */
+#define MZ_K_DEC_EMBED 11  /* decoder step kernels (eager steps): token + position embedding + LayerNorm */
+#define MZ_K_DEC_QKV 12    /* self-attention q/k/v projection (k, v into the cache) */
+#define MZ_K_DEC_SELF 13   /* self-attention over the cache */
+#define MZ_K_DEC_OPROJ 14  /* self-attention out-projection (split-K partials) */
+#define MZ_K_DEC_ADDLN 15  /* residual add of the partials + LayerNorm */
+#define MZ_K_DEC_CROSS 16  /* cross-attention (its query projection and the alignment rows included) */
+#define MZ_K_DEC_XO 17     /* cross-attention out-projection */
+#define MZ_K_DEC_FC1 18    /* fc1 + GELU */
+#define MZ_K_DEC_FC2 19    /* fc2 (split-K partials) */
+#define MZ_K_DEC_LM 20     /* tied LM head with the per-workgroup argmax partials */
+#define MZ_K_DEC_ARGMAX 21 /* greedy choice */
 int mz_engine_profile(mz_engine* e, int on);
 int mz_engine_profile_read(mz_engine* e, int kernel, double* total_ms, int* count);
 

@@ -46,7 +46,9 @@ EPI_F16, EPI_GELU_F16, EPI_RESID_F32, EPI_GELU_POS, EPI_HEADS = range(5)
  BUF_DEC_TRACE, BUF_SELF_K, BUF_SELF_V) = range(13)
 DT_F16, DT_F32 = 0, 1
 # kernel classes of mz_engine_profile_read
-K_NAMES = ["mel", "conv1", "conv2", "ln", "qkv", "attn", "oproj", "fc1", "fc2", "xkv", "step"]
+K_NAMES = ["mel", "conv1", "conv2", "ln", "qkv", "attn", "oproj", "fc1", "fc2", "xkv", "step",
+           "dec_embed", "dec_qkv", "dec_self", "dec_oproj", "dec_addln", "dec_cross", "dec_xo", "dec_fc1", "dec_fc2",
+           "dec_lm", "dec_argmax"]
 
 # name -> (restype, argtypes); every int-returning function is a status
 SIGNATURES = {

@@ -647,9 +647,10 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
     hipStream_t s = e->c->stream;
     const int D = e->dm.d, F = e->dm.ff, nh = e->dm.nh, nl = e->dm.dec_layers, mt = e->dm.max_t, V = e->dm.vocab;
     const long blk = (long)TPAD * HD;
-    TRY(mz_dec_embed_ln_launch(s, e->tok, e->ctr, e->emb, e->dpos, e->x, e->decv[0].ln1.w, e->decv[0].ln1.b, e->h, b, D,
-                               mt, EPS),
-        "embed");
+    PROF(MZ_K_DEC_EMBED,
+         mz_dec_embed_ln_launch(s, e->tok, e->ctr, e->emb, e->dpos, e->x, e->decv[0].ln1.w, e->decv[0].ln1.b, e->h, b,
+                                D, mt, EPS),
+         "embed");
     // with the trace on (eager steps only): the residual entering layer l, l = 0 .. nl (nl: after the last layer)
     const bool dtr = e->trace_on && e->dtrace && !e->capturing;
     auto dtrace = [&](int l) {
@@ -719,21 +720,28 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
             g.ctr = e->ctr;
             g.maxT = mt;
             g.d = D;
-            TRY(mz_dec_gemm_launch(s, DEPI_QKV, g), "dec qkv");
+            PROF(MZ_K_DEC_QKV, mz_dec_gemm_launch(s, DEPI_QKV, g), "dec qkv");
         }
-        TRY(attn(e->q, 1, nullptr, nullptr, kc, vc, (long)nh * mt * HD, -1, nullptr), "self attention");
-        TRY(gemm(DEPI_PARTIAL, e->datt, D, L.o, D, D, ks_dd, e->part, D), "dec out-proj");
-        TRY(mz_dec_add_ln_launch(s, e->x, e->part, ks_dd, (long)b * D, L.o.b, L.lnx.w, L.lnx.b, e->h, b, D, EPS), "add+ln");
+        PROF(MZ_K_DEC_SELF, attn(e->q, 1, nullptr, nullptr, kc, vc, (long)nh * mt * HD, -1, nullptr), "self attention");
+        PROF(MZ_K_DEC_OPROJ, gemm(DEPI_PARTIAL, e->datt, D, L.o, D, D, ks_dd, e->part, D), "dec out-proj");
+        PROF(MZ_K_DEC_ADDLN,
+             mz_dec_add_ln_launch(s, e->x, e->part, ks_dd, (long)b * D, L.o.b, L.lnx.w, L.lnx.b, e->h, b, D, EPS),
+             "add+ln");
         // the cross-attention projects its own query from the layer-norm output
-        TRY(attn(nullptr, 0, L.xq.w, L.xq.b, e->xkvbuf + (size_t)(2 * i) * nh * blk,
-                 e->xkvbuf + (size_t)(2 * i + 1) * nh * blk, (long)nl * 2 * nh * blk, TENC, e->aslot + (size_t)i * nh),
-            "cross attention");
-        TRY(gemm(DEPI_PARTIAL, e->datt, D, L.xo, D, D, ks_dd, e->part, D), "dec cross out-proj");
-        TRY(mz_dec_add_ln_launch(s, e->x, e->part, ks_dd, (long)b * D, L.xo.b, L.ln3.w, L.ln3.b, e->h, b, D, EPS), "add+ln");
-        TRY(gemm(DEPI_GELU_F16, e->h, D, L.fc1, F, D, 1, e->dff, F), "dec fc1");
-        TRY(gemm(DEPI_PARTIAL, e->dff, F, L.fc2, D, F, ks_df, e->part, D), "dec fc2");
+        PROF(MZ_K_DEC_CROSS,
+             attn(nullptr, 0, L.xq.w, L.xq.b, e->xkvbuf + (size_t)(2 * i) * nh * blk,
+                  e->xkvbuf + (size_t)(2 * i + 1) * nh * blk, (long)nl * 2 * nh * blk, TENC, e->aslot + (size_t)i * nh),
+             "cross attention");
+        PROF(MZ_K_DEC_XO, gemm(DEPI_PARTIAL, e->datt, D, L.xo, D, D, ks_dd, e->part, D), "dec cross out-proj");
+        PROF(MZ_K_DEC_ADDLN,
+             mz_dec_add_ln_launch(s, e->x, e->part, ks_dd, (long)b * D, L.xo.b, L.ln3.w, L.ln3.b, e->h, b, D, EPS),
+             "add+ln");
+        PROF(MZ_K_DEC_FC1, gemm(DEPI_GELU_F16, e->h, D, L.fc1, F, D, 1, e->dff, F), "dec fc1");
+        PROF(MZ_K_DEC_FC2, gemm(DEPI_PARTIAL, e->dff, F, L.fc2, D, F, ks_df, e->part, D), "dec fc2");
         const Ln& nx = i + 1 < nl ? e->decv[i + 1].ln1 : e->dln;
-        TRY(mz_dec_add_ln_launch(s, e->x, e->part, ks_df, (long)b * D, L.fc2.b, nx.w, nx.b, e->h, b, D, EPS), "add+ln");
+        PROF(MZ_K_DEC_ADDLN,
+             mz_dec_add_ln_launch(s, e->x, e->part, ks_df, (long)b * D, L.fc2.b, nx.w, nx.b, e->h, b, D, EPS),
+             "add+ln");
         if (dtr) TRY(dtrace(i + 1), "decoder trace");
     }
     // tied LM head with the masked per-workgroup argmax, then the greedy choice, which advances the position
@@ -754,9 +762,11 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
         g.bs2 = lang ? -1 : e->bs2;
         g.prompt_len = prompt_len;
         g.amax = e->amax;
-        TRY(mz_dec_gemm_launch(s, DEPI_LOGITS, g), "lm head");
+        PROF(MZ_K_DEC_LM, mz_dec_gemm_launch(s, DEPI_LOGITS, g), "lm head");
     }
-    TRY(mz_dec_argmax_launch(s, e->amax, mz_lm_blocks(V), e->tok, e->done, e->ctr, b, mt, prompt_len, e->eos), "argmax");
+    PROF(MZ_K_DEC_ARGMAX,
+         mz_dec_argmax_launch(s, e->amax, mz_lm_blocks(V), e->tok, e->done, e->ctr, b, mt, prompt_len, e->eos),
+         "argmax");
     return MZ_OK;
 }
 

@@ -405,7 +405,7 @@ __global__ void __launch_bounds__(256) dec_lmhead_kernel(const MzDec p, int T) {
 // The cross-attention's query projection runs in the same workgroup (wq set): its head's 64 rows of wq (read by the
 // 32 rows' workgroups of that head, so from L2 after the first) against the row's layer-norm output staged in LDS,
 // 8 lanes per weight row over whole 128-byte lines, with the first keys and values in flight behind them.
-template <int AG, int AU>
+template <int AG, int AU, bool CROSS>
 __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
     __shared__ float qs[MZ_HD];
     __shared__ __attribute__((aligned(16))) f16 xs[MZ_DEC_KSLICE];
@@ -419,7 +419,7 @@ __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
     const int tid = threadIdx.x, grp = tid >> 3, sub = tid & 7;
     const int pos = a.ctr[1];
     const int L = a.L > 0 ? a.L : min(pos + 1, a.maxT);
-    const int slot = a.aslot ? a.aslot[head] : -1;
+    const int slot = CROSS && a.aslot ? a.aslot[head] : -1;
 
     // the first batch of keys and values is requested before the query, which arrives in the same round trip
     const f16* kb = a.k + (long)b * a.kv_b + (long)head * a.kv_h + sub * 8;
@@ -435,7 +435,7 @@ __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
         }
     };
     constexpr float QS = 0.125f * 1.4426950408889634f;  // 1/8 and log2(e)
-    if (AG * 8 == 256 && a.wq) {
+    if (CROSS && AG * 8 == 256 && a.wq) {
         // q[i] = xin[b] . wq[head * 64 + i] + qbias: lane (r8, q8) of wave w takes rows 8 w + r8 and 32 + 8 w + r8,
         // 16-byte chunks q8, q8 + 8, ... of each (nj per row); 8 lanes sum one row through DPP
         const int w = tid >> 6, r8 = (tid >> 3) & 7, q8 = tid & 7, nj = a.d >> 6;
@@ -641,10 +641,11 @@ hipError_t mz_dec_attn_launch(hipStream_t s, const MzDecAttn& a) {
     if (a.aslot && (!a.align || a.na <= 0 || (a.L > 0 && a.L != MZ_TENC))) return hipErrorInvalidValue;
     // the fused query projection: cross-attention only, whole 64-half chunks per lane group, the row in LDS
     if (a.wq && (a.L <= 0 || !a.xin || a.d % 64 != 0 || a.d > MZ_DEC_KSLICE)) return hipErrorInvalidValue;
+    // two instances (the query projection compiled only into the cross one), also told apart by name in traces
     if (a.L > 0)
-        hipLaunchKernelGGL((dec_attn_kernel<32, 8>), dim3(a.B * a.nh), dim3(32 * 8), 0, s, a);
+        hipLaunchKernelGGL((dec_attn_kernel<32, 8, true>), dim3(a.B * a.nh), dim3(32 * 8), 0, s, a);
     else
-        hipLaunchKernelGGL((dec_attn_kernel<32, 8>), dim3(a.B * a.nh), dim3(32 * 8), 0, s, a);
+        hipLaunchKernelGGL((dec_attn_kernel<32, 8, false>), dim3(a.B * a.nh), dim3(32 * 8), 0, s, a);
     return hipGetLastError();
 }
 
