@@ -123,9 +123,11 @@ def probe(name: str, reps: int = 5):
     def f16(shape, sc=1.0):
         return (rng.standard_normal(shape, dtype=np.float32) * sc).astype(np.float16)
 
-    if name == "dec_step":
+    name_graph = name == "dec_graph"
+    if name in ("dec_step", "dec_graph"):
         # three eager turbo decoder steps at B = 32 from position 200 (random self cache and cross keys/values):
-        # the decoder kernels at the benchmark's step shape, one dispatch each per layer and step
+        # the decoder kernels at the benchmark's step shape, one dispatch each per layer and step ("dec_graph":
+        # twenty replays of the captured step instead)
         gd = synth.Geometry(d=d, ff=ff, nh=nh, enc_layers=1, dec_layers=g.dec_layers, n_mels=g.n_mels, vocab=g.vocab)
         W = synth.random_weights(gd, seed=0)
         gen = synth.generation_config(gd, align_heads=synth.generation_config(g)["alignment_heads"])
@@ -141,10 +143,15 @@ def probe(name: str, reps: int = 5):
         e.reset(toks[:, :1])
         ctx.upload(e.buffer(L.BUF_TOK)[0], toks)
         ctx.upload(e.buffer(L.BUF_CTR)[0], np.array([200, 0, 0, 0], np.int32))
-        for _ in range(3):
-            e.step(N_CLIPS, False, 1)
+        if name_graph:  # the captured step replayed 20 times (the benchmark's own launch path)
+            e.capture(N_CLIPS, 1)
+            for _ in range(20):
+                e.replay()
+        else:
+            for _ in range(3):
+                e.step(N_CLIPS, False, 1)
         ctx.sync()
-        print(json.dumps({"probe": name, "steps": 3, "position": 200,
+        print(json.dumps({"probe": name, "steps": 20 if name_graph else 3, "position": 200,
                           "dec_cross_bytes": dec_kernel_bytes(g, N_CLIPS, 201, 6)["dec_cross"]}))
         e.close()
         return
@@ -235,6 +242,14 @@ def run_model(g, seed: int, steps: int, warmup: int, graph: bool, label: str, L,
          "enc_s": float(np.mean([t.enc for t in tms])), "dec_s": float(np.mean([t.dec for t in tms])),
          "post_s": float(np.mean([t.post for t in tms])), "nsteps": tms[-1].steps, "na": len(gen["alignment_heads"])}
     log(f"bench: {label}: {steps} steps in {dt:.3f}s = {r['ms_step']:.1f} ms/step, {r['value']:.0f} audio-s/s")
+    # the same steps with the log-mel handed over in host memory (staged through the engine's pinned buffers): the
+    # PCIe-inclusive rate, outside the headline value
+    t0 = time.perf_counter()
+    for i in range(2):
+        transcribe.transcribe(e, mel, prompt, max_new=MAX_NEW, graph=graph)
+    ctx.sync()
+    r["host_mel_value"] = N_CLIPS * 30.0 / ((time.perf_counter() - t0) / 2)
+    log(f"bench: {label} with host log-mel: {r['host_mel_value']:.0f} audio-s/s")
 
     # encoder kernels, HIP events around every launch: the transcription overlaps two encoder groups on two streams,
     # so each kernel class is timed in one more encoder pass over the same clips with the groups one after the other
@@ -417,6 +432,9 @@ def main():
         "decode_step_us": round(r["step_us"], 2),
         "decode_step_hbm_frac": round(r["step_bytes"] / (r["step_us"] * 1e-6) / PEAK_HBM, 4),
         "decode_step_us_e2e_avg": round(r["dec_s"] / r["nsteps"] * 1e6, 2),
+        "host_mel_audio_s_per_s": round(r["host_mel_value"], 2),
+        "host_mel_note": "the same step with the log-mel in host memory (pinned staging, asynchronous copies per "
+                         "encoder lane), 2 steps: the PCIe-inclusive rate, not the headline value",
         "kernels": kernels,
         "kernel_timing": "HIP events around every launch: the encoder classes in one extra encoder pass over the 32 "
                          "clips with the groups one after the other on one stream (the timed steps overlap two "

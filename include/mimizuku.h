@@ -146,9 +146,12 @@ int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, int bmax, int
 #define MZ_DT_F32 1
 /* Places one checkpoint tensor by its Hugging Face name (Loader, src/model.rs:200-265): shape-checked, F32
  * converted to F16, q/k/v fused (zero k bias), every decoder layer's cross k/v fused, conv weights reordered
- * tap-major. Unknown names are ignored. */
+ * tap-major. Unknown names are ignored. The data is converted into two pinned 32 MB staging buffers in turn, each
+ * one's copy to the device in flight while the next chunk is converted (the reference's Arena, src/gpu.rs:289-374);
+ * `data` may be reused when the call returns. */
 int mz_engine_put(mz_engine* e, const char* name, int dtype, const void* data, const int64_t* shape, int ndim);
-/* Checks every tensor was placed (Arena::finish, src/gpu.rs:363-373). */
+/* Checks every tensor was placed, waits for the uploads and frees the staging buffers (Arena::finish,
+ * src/gpu.rs:363-373). */
 int mz_engine_finish(mz_engine* e);
 /* Every tensor of <model_dir>/model.safetensors through mz_engine_put, then mz_engine_finish (the Loader over the
  * mapped checkpoint, src/model.rs:200-265 with src/st.rs; F16 and F32 tensors, anything else is an error). */
@@ -157,7 +160,8 @@ int mz_engine_load(mz_engine* e, const char* model_dir);
  * through mz_model_open, mz_engine_new, then mz_engine_load. */
 int mz_engine_open(mz_ctx* c, const char* model_dir, int bmax, int eg, mz_engine** out);
 /* Encoder for n <= eg clips of log-mel f32 [n][n_mels][3000] (host); writes every decoder layer's cross k/v into
- * decoder slots slot0 .. slot0 + n - 1 (Engine::encode, src/model.rs:545-625). */
+ * decoder slots slot0 .. slot0 + n - 1 (Engine::encode, src/model.rs:545-625). The log-mel goes through a pinned
+ * buffer of the engine and an asynchronous copy (the host array may be reused when the call returns). */
 int mz_engine_encode(mz_engine* e, const float* mels, int n, int slot0);
 /* As mz_engine_encode with the log-mel already in device memory (f32 [n][n_mels][3000] at `mels`): no host copy. */
 int mz_engine_encode_device(mz_engine* e, uint64_t mels, int n, int slot0);

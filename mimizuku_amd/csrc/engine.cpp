@@ -62,6 +62,50 @@ struct EncBufs {
     float* ex;
 };
 
+// Pinned host staging for uploads (the reference's Arena, src/gpu.rs:289-374, stages weights through two pinned
+// buffers): data is written into one buffer while the other's copy to the device is in flight, each buffer's copy
+// marked by an event that the next writer of that buffer waits for.
+struct Staging {
+    static constexpr size_t CAP = (size_t)32 << 20;  // bytes per buffer
+    void* buf[2] = {};
+    hipEvent_t ev[2] = {};
+    int next = 0;
+    int init() {
+        if (buf[0]) return MZ_OK;
+        for (int i = 0; i < 2; i++) {
+            if (int r = mz_hip(hipHostMalloc(&buf[i], CAP, hipHostMallocDefault), "hipHostMalloc (staging)")) return r;
+            if (int r = mz_hip(hipEventCreateWithFlags(&ev[i], hipEventDisableTiming), "hipEventCreate")) return r;
+        }
+        return MZ_OK;
+    }
+    // the buffer the next chunk goes into, once its previous copy has finished
+    int acquire(void** p) {
+        if (int r = mz_hip(hipEventSynchronize(ev[next]), "staging wait")) return r;
+        *p = buf[next];
+        return MZ_OK;
+    }
+    int submit(void* dst, size_t bytes, hipStream_t s) {
+        if (int r = mz_hip(hipMemcpyAsync(dst, buf[next], bytes, hipMemcpyHostToDevice, s), "staged upload")) return r;
+        if (int r = mz_hip(hipEventRecord(ev[next], s), "hipEventRecord")) return r;
+        next ^= 1;
+        return MZ_OK;
+    }
+    void release() {
+        for (int i = 0; i < 2; i++) {
+            if (ev[i]) {
+                hipEventSynchronize(ev[i]);
+                hipEventDestroy(ev[i]);
+                ev[i] = nullptr;
+            }
+            if (buf[i]) {
+                hipHostFree(buf[i]);
+                buf[i] = nullptr;
+            }
+        }
+        next = 0;
+    }
+};
+
 struct mz_engine {
     mz_ctx* c = nullptr;
     mz_dims dm{};
@@ -77,6 +121,11 @@ struct mz_engine {
     size_t arena_elems = 0, arena_used = 0;
     std::map<std::string, Slot> slots;
     std::set<std::string> placed;
+    Staging wstage;  // weight uploads, until mz_engine_finish
+    // host log-mel of a group staged per encoder lane (pinned, allocated at the first host upload), and the event of
+    // its last copy
+    float* mel_pin[MZ_ENC_LANES] = {};
+    hipEvent_t mel_ev[MZ_ENC_LANES] = {};
     EncLayer* enc = nullptr;
     DecLayer* dec = nullptr;
     std::vector<EncLayer> encv;
@@ -397,24 +446,38 @@ extern "C" int mz_engine_put(mz_engine* e, const char* name, int dtype, const vo
         return mz_fail(MZ_ERR_ARG, "%s has shape [%s], expected [%s]", name, got.c_str(), want.c_str());
     }
     if (dtype != MZ_DT_F16 && dtype != MZ_DT_F32) return mz_fail(MZ_ERR_ARG, "%s: unsupported dtype %d", name, dtype);
+    // element i of the source as binary16 bits
+    const uint16_t* h = (const uint16_t*)data;
+    const float* f = (const float*)data;
+    auto src = [&](size_t i) { return dtype == MZ_DT_F16 ? h[i] : mz_f2h_host(f[i]); };
+    // the destination layout, rows of `cols` halves: the tensor itself (one row), or a conv weight [co][ci][3]
+    // reordered tap-major into rows [co][kpad] (column tap * ci + ci_index, zero padding after 3 ci)
     size_t n = 1;
     for (auto v : s.shape) n *= (size_t)v;
-    std::vector<uint16_t> h16(n);
-    if (dtype == MZ_DT_F16) {
-        std::memcpy(h16.data(), data, n * 2);
-    } else {
-        const float* f = (const float*)data;
-        for (size_t i = 0; i < n; i++) h16[i] = mz_f2h_host(f[i]);
+    const bool conv = s.kind == 1;
+    const size_t ci = conv ? (size_t)s.shape[1] : 0, cols = conv ? (size_t)s.kpad : n, rows = conv ? (size_t)s.shape[0] : 1;
+    // converted chunk by chunk into the pinned staging buffers, each chunk's copy in flight while the next is written
+    if (int r = e->wstage.init()) return r;
+    const size_t per = Staging::CAP / 2;  // halves per chunk
+    const size_t total = rows * cols;
+    for (size_t o0 = 0; o0 < total; o0 += per) {
+        const size_t k = std::min(per, total - o0);
+        void* pv;
+        if (int r = e->wstage.acquire(&pv)) return r;
+        uint16_t* out = (uint16_t*)pv;
+        if (!conv) {
+            if (dtype == MZ_DT_F16)
+                std::memcpy(out, h + o0, k * 2);
+            else
+                for (size_t i = 0; i < k; i++) out[i] = mz_f2h_host(f[o0 + i]);
+        } else {
+            for (size_t i = 0; i < k; i++) {
+                const size_t o = (o0 + i) / cols, c = (o0 + i) % cols, t = c / ci, cc = c % ci;
+                out[i] = t < 3 ? src((o * ci + cc) * 3 + t) : (uint16_t)0;
+            }
+        }
+        if (int r = e->wstage.submit(s.dst + o0, k * 2, e->c->stream)) return r;
     }
-    if (s.kind == 1) {  // conv weight [co][ci][3] -> [co][kpad], column tap * ci_n + ci
-        const size_t co = s.shape[0], ci = s.shape[1];
-        std::vector<uint16_t> w((size_t)co * s.kpad, 0);
-        for (size_t o = 0; o < co; o++)
-            for (size_t i = 0; i < ci; i++)
-                for (size_t t = 0; t < 3; t++) w[o * s.kpad + t * ci + i] = h16[(o * ci + i) * 3 + t];
-        h16.swap(w);
-    }
-    if (int r = mz_upload(e->c, (uint64_t)(uintptr_t)s.dst, h16.data(), h16.size() * 2)) return r;
     e->placed.insert(name);
     return MZ_OK;
 }
@@ -423,6 +486,8 @@ extern "C" int mz_engine_finish(mz_engine* e) {
     if (!e) return mz_fail(MZ_ERR_ARG, "mz_engine_finish: null engine");
     for (auto& kv : e->slots)
         if (!e->placed.count(kv.first)) return mz_fail(MZ_ERR_STATE, "model tensor %s was not provided", kv.first.c_str());
+    if (int r = mz_sync(e->c)) return r;
+    e->wstage.release();  // the staging goes once every weight is in place (Arena::finish)
     e->loaded = true;
     return MZ_OK;
 }
@@ -472,7 +537,19 @@ static int encode_impl(mz_engine* e, const float* mels, bool on_device, int n, i
     const int rows = n * TENC;
     const float* src = mels;
     if (!on_device) {
-        TRY(hipMemcpyAsync(B.mel, mels, (size_t)n * nm * NFR * 4, hipMemcpyHostToDevice, s), "mel upload");
+        // through this lane's pinned buffer: the host copy waits only for the lane's previous upload, and the
+        // transfer itself is asynchronous (overlapping the other lane's encoder work)
+        const size_t bytes = (size_t)n * nm * NFR * 4;
+        if (!e->mel_pin[lane]) {
+            TRY(hipHostMalloc((void**)&e->mel_pin[lane], (size_t)e->eg * nm * NFR * 4, hipHostMallocDefault),
+                "hipHostMalloc (mel)");
+            TRY(hipEventCreateWithFlags(&e->mel_ev[lane], hipEventDisableTiming), "hipEventCreate");
+        } else {
+            TRY(hipEventSynchronize(e->mel_ev[lane]), "mel staging wait");
+        }
+        std::memcpy(e->mel_pin[lane], mels, bytes);
+        TRY(hipMemcpyAsync(B.mel, e->mel_pin[lane], bytes, hipMemcpyHostToDevice, s), "mel upload");
+        TRY(hipEventRecord(e->mel_ev[lane], s), "hipEventRecord");
         src = B.mel;
     }
     PROF(MZ_K_MEL, mz_mel_transpose_launch(s, src, B.melT, n, nm), "mel transpose");
@@ -873,6 +950,14 @@ extern "C" int mz_engine_free(mz_engine* e) {
         hipEventDestroy(r.b);
     }
     for (hipEvent_t x : e->evpool) hipEventDestroy(x);
+    e->wstage.release();
+    for (int k = 0; k < MZ_ENC_LANES; k++) {
+        if (e->mel_ev[k]) {
+            hipEventSynchronize(e->mel_ev[k]);
+            hipEventDestroy(e->mel_ev[k]);
+        }
+        if (e->mel_pin[k]) hipHostFree(e->mel_pin[k]);
+    }
     if (e->fork) hipEventDestroy(e->fork);
     for (int k = 0; k < MZ_ENC_LANES - 1; k++) {
         if (e->ls[k]) {
