@@ -249,6 +249,17 @@ int mz_transcribe(mz_engine* e, const float* mels, const int32_t* frames, int n,
 int mz_transcribe_device(mz_engine* e, uint64_t mels, const int32_t* frames, int n, const int32_t* prompt,
                          int prompt_len, int detect, int use_graph, int max_new, int half_align, int32_t* seq,
                          int32_t* seq_len, float* ts, int32_t* langs, mz_times* times);
+/* mz_transcribe in two halves (transcribe, src/transcribe.rs:107-116 and 118-167): submit enqueues the encoder of a
+ * chunk of n <= bmax clips and returns at once, so the caller's host work (reading and resampling the next files)
+ * overlaps it; collect decodes that chunk and returns exactly what mz_transcribe returns (same arguments and outputs;
+ * n must be the submitted count). One chunk at a time: submit refuses while a chunk is pending, and so does
+ * mz_transcribe. A host log-mel is copied before submit returns; a device log-mel must stay unchanged until collect.
+ * times->enc = the host's time in submit plus its wait in collect for the encoder. */
+int mz_transcribe_submit(mz_engine* e, const float* mels, int n);
+int mz_transcribe_submit_device(mz_engine* e, uint64_t mels, int n);
+int mz_transcribe_collect(mz_engine* e, const int32_t* frames, int n, const int32_t* prompt, int prompt_len,
+                          int detect, int use_graph, int max_new, int half_align, int32_t* seq, int32_t* seq_len,
+                          float* ts, int32_t* langs, mz_times* times);
 
 /* Token start times of n clips on the device, the same bits as mz_jump_times on each clip (jump_times,
  * src/align.rs:8-63; the reference runs it on the host after downloading the weights, transcribe.rs:150-158).

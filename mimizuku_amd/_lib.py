@@ -112,6 +112,9 @@ SIGNATURES = {
     "mz_engine_free": (i32, [P]),
     "mz_transcribe": (i32, [P, P, P, i32, P, i32, i32, i32, i32, i32, P, P, P, P, C.POINTER(Times)]),
     "mz_transcribe_device": (i32, [P, u64, P, i32, P, i32, i32, i32, i32, i32, P, P, P, P, C.POINTER(Times)]),
+    "mz_transcribe_submit": (i32, [P, P, i32]),
+    "mz_transcribe_submit_device": (i32, [P, u64, i32]),
+    "mz_transcribe_collect": (i32, [P, P, i32, P, i32, i32, i32, i32, i32, P, P, P, P, C.POINTER(Times)]),
     "mz_wav_read": (i32, [C.c_char_p, P, sz, C.POINTER(sz), C.POINTER(i32)]),
     "mz_resample_16k": (i32, [P, sz, i32, P, sz, C.POINTER(sz)]),
     "mz_mel_tables": (i32, [i32, P, P, P]),

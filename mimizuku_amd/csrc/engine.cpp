@@ -158,6 +158,11 @@ struct mz_engine {
     size_t part_elems = 0;
     mz_graph* graph = nullptr;
     int graph_b = -1, graph_np = -1;
+    // the chunk submitted and not yet collected (mz_transcribe_submit / mz_transcribe_collect): its clip count (0:
+    // none) and the host time spent enqueueing its encoder; enc_done marks its encoder done
+    int pending_n = 0;
+    double pending_enq = 0;
+    hipEvent_t enc_done = nullptr;
     // kernel timing (mz_engine_profile): events around each encoder launch and each decoder step
     bool prof_on = false;
     struct Rec {
@@ -213,6 +218,9 @@ size_t weight_elems(const mz_dims& d, int* k1pad) {
     n += r((size_t)d.vocab * D) + r((size_t)d.max_t * D) + 2 * r(D);
     return n;
 }
+
+// one set of cross keys/values: [bmax][dec layers][k|v][heads] tiles of 1536 x 64
+size_t xkv_elems(const mz_dims& d, int bmax) { return (size_t)bmax * d.dec_layers * 2 * d.nh * (size_t)TPAD * HD; }
 
 int ksplit_for(int N, int K) {
     // Split K over workgroups until the grid covers most of the 256 CUs, with at most 16 groups of 64 per workgroup
@@ -391,7 +399,8 @@ extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, in
             (r = mz_hip(hipEventCreateWithFlags(&e->join[k], hipEventDisableTiming), "hipEventCreate")))
             return fail(r);
     }
-    if ((r = e->alloc(&e->xkvbuf, B * nl * 2 * nh * (size_t)TPAD * HD)) || (r = e->alloc(&e->tok, B * mt)) ||
+    if ((r = mz_hip(hipEventCreateWithFlags(&e->enc_done, hipEventDisableTiming), "hipEventCreate"))) return fail(r);
+    if ((r = e->alloc(&e->xkvbuf, xkv_elems(*d, bmax))) || (r = e->alloc(&e->tok, B * mt)) ||
         (r = e->alloc(&e->done, B)) || (r = e->alloc(&e->ctr, 4)) || (r = e->alloc(&e->x, B * D)) ||
         (r = e->alloc(&e->q, B * D)) || (r = e->alloc(&e->h, B * D)) || (r = e->alloc(&e->datt, B * D)) ||
         (r = e->alloc(&e->dff, B * F)) || (r = e->alloc(&e->kc, (size_t)nl * B * nh * mt * HD)) ||
@@ -524,13 +533,15 @@ extern "C" int mz_engine_set_trace(mz_engine* e, int on) {
         }                                                                           \
     } while (0)
 
-static int encode_impl(mz_engine* e, const float* mels, bool on_device, int n, int slot0, int lane = 0) {
+// One encoder group of n clips into cross k/v slots slot0.. of `xkv`, on stream s with lane `lane`'s scratch and
+// pinned staging (lane 0: the engine's own scratch).
+static int encode_impl(mz_engine* e, const float* mels, bool on_device, int n, int slot0, int lane, hipStream_t s,
+                       f16* xkv) {
     if (!e || !mels) return mz_fail(MZ_ERR_ARG, "mz_engine_encode: null argument");
     if (!e->loaded) return mz_fail(MZ_ERR_STATE, "mz_engine_encode: weights not loaded (mz_engine_finish)");
     if (n <= 0 || n > e->eg || slot0 < 0 || slot0 + n > e->bmax)
         return mz_fail(MZ_ERR_ARG, "mz_engine_encode: %d clips at slot %d (enc group %d, bmax %d)", n, slot0, e->eg, e->bmax);
     if (lane && e->trace_on) return mz_fail(MZ_ERR_STATE, "encoder trace on an extra lane");
-    hipStream_t s = lane ? e->ls[lane - 1] : e->c->stream;
     const EncBufs B =
         lane ? e->lanes[lane - 1] : EncBufs{e->mel, e->melT, e->h1, e->hb, e->qkvh, e->att, e->ff, e->dd, e->ex};
     const int D = e->dm.d, nm = e->dm.n_mels, nh = e->dm.nh, F = e->dm.ff, nl = e->dm.dec_layers;
@@ -646,7 +657,7 @@ static int encode_impl(mz_engine* e, const float* mels, bool on_device, int n, i
     g.M = rows;
     g.N = nl * 2 * D;
     g.K = D;
-    g.heads = e->xkvbuf;
+    g.heads = xkv;
     g.blocks_per_clip = nl * 2 * nh;
     g.nh = nh;
     g.kind = 2;
@@ -656,11 +667,13 @@ static int encode_impl(mz_engine* e, const float* mels, bool on_device, int n, i
 }
 
 extern "C" int mz_engine_encode(mz_engine* e, const float* mels, int n, int slot0) {
-    return encode_impl(e, mels, false, n, slot0);
+    if (!e) return mz_fail(MZ_ERR_ARG, "mz_engine_encode: null engine");
+    return encode_impl(e, mels, false, n, slot0, 0, e->c->stream, e->xkvbuf);
 }
 
 extern "C" int mz_engine_encode_device(mz_engine* e, uint64_t mels, int n, int slot0) {
-    return encode_impl(e, (const float*)(uintptr_t)mels, true, n, slot0);
+    if (!e) return mz_fail(MZ_ERR_ARG, "mz_engine_encode: null engine");
+    return encode_impl(e, (const float*)(uintptr_t)mels, true, n, slot0, 0, e->c->stream, e->xkvbuf);
 }
 
 extern "C" int mz_engine_profile(mz_engine* e, int on) {
@@ -776,6 +789,7 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
         return mz_dec_attn_launch(s, a);
     };
     const int ks_dd = ksplit_for(D, D), ks_df = ksplit_for(D, F);
+    const f16* xkv = e->xkvbuf;
     for (int i = 0; i < nl; i++) {
         const DecLayer& L = e->decv[i];
         f16* kc = e->kc + (size_t)i * e->bmax * nh * mt * HD;
@@ -806,8 +820,8 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
              "add+ln");
         // the cross-attention projects its own query from the layer-norm output
         PROF(MZ_K_DEC_CROSS,
-             attn(nullptr, 0, L.xq.w, L.xq.b, e->xkvbuf + (size_t)(2 * i) * nh * blk,
-                  e->xkvbuf + (size_t)(2 * i + 1) * nh * blk, (long)nl * 2 * nh * blk, TENC, e->aslot + (size_t)i * nh),
+             attn(nullptr, 0, L.xq.w, L.xq.b, xkv + (size_t)(2 * i) * nh * blk, xkv + (size_t)(2 * i + 1) * nh * blk,
+                  (long)nl * 2 * nh * blk, TENC, e->aslot + (size_t)i * nh),
              "cross attention");
         PROF(MZ_K_DEC_XO, gemm(DEPI_PARTIAL, e->datt, D, L.xo, D, D, ks_dd, e->part, D), "dec cross out-proj");
         PROF(MZ_K_DEC_ADDLN,
@@ -917,7 +931,7 @@ extern "C" int mz_engine_buffer(mz_engine* e, int which, uint64_t* dptr, size_t*
             if (!e->trace) return mz_fail(MZ_ERR_STATE, "trace not enabled");
             p = e->trace, n = (size_t)e->dm.enc_layers * G * TENC * D * 4;
             break;
-        case MZ_BUF_XKV: p = e->xkvbuf, n = B * e->dm.dec_layers * 2 * e->dm.nh * (size_t)TPAD * HD * 2; break;
+        case MZ_BUF_XKV: p = e->xkvbuf, n = xkv_elems(e->dm, e->bmax) * 2; break;
         case MZ_BUF_DEC_X: p = e->x, n = B * D * 4; break;
         case MZ_BUF_ENC_X: p = e->ex, n = G * TENC * D * 4; break;
         case MZ_BUF_DEC_TRACE:
@@ -945,6 +959,7 @@ extern "C" int mz_engine_free(mz_engine* e) {
     if (!e) return MZ_OK;
     if (e->graph) mz_graph_free(e->graph);
     hipStreamSynchronize(e->c->stream);
+    if (e->enc_done) hipEventDestroy(e->enc_done);
     for (auto& r : e->recs) {
         hipEventDestroy(r.a);
         hipEventDestroy(r.b);
@@ -986,38 +1001,67 @@ extern "C" int mz_engine_free(mz_engine* e) {
 
 // ------------------------------------------------------------------ batch transcription (src/transcribe.rs:104-167)
 
-static int transcribe_impl(mz_engine* e, const float* mels, bool on_device, const int32_t* frames, int n,
-                           const int32_t* prompt, int prompt_len, int detect, int use_graph, int max_new,
-                           int half_align, int32_t* seq, int32_t* seq_len, float* ts, int32_t* langs,
-                           mz_times* times) {
-    using clk = std::chrono::steady_clock;
-    if (!e || !mels || !frames || !prompt || !seq || !seq_len || !ts || !langs)
-        return mz_fail(MZ_ERR_ARG, "mz_transcribe: null argument");
-    if (n <= 0 || n > e->bmax) return mz_fail(MZ_ERR_ARG, "mz_transcribe: %d clips (bmax %d)", n, e->bmax);
+using clk = std::chrono::steady_clock;
+static double since(clk::time_point a) { return std::chrono::duration<double>(clk::now() - a).count(); }
+
+// Enqueues the encoder of a chunk of n clips and returns (the first half of transcribe, src/transcribe.rs:107-116):
+// its groups go round-robin over two lanes (the main stream and the engine's second stream, each with its own
+// scratch), and one event marks them all done. One chunk at a time: collect it before submitting the next.
+static int submit_impl(mz_engine* e, const float* mels, bool on_device, int n) {
+    if (!e || !mels) return mz_fail(MZ_ERR_ARG, "mz_transcribe_submit: null argument");
+    if (!e->loaded) return mz_fail(MZ_ERR_STATE, "mz_transcribe_submit: weights not loaded (mz_engine_finish)");
+    if (n <= 0 || n > e->bmax) return mz_fail(MZ_ERR_ARG, "mz_transcribe_submit: %d clips (bmax %d)", n, e->bmax);
+    if (e->pending_n) return mz_fail(MZ_ERR_STATE, "mz_transcribe_submit: a chunk is pending; collect it first");
+    const auto t0 = clk::now();
+    const int nm = e->dm.n_mels, ngroups = (n + e->eg - 1) / e->eg;
+    const int nlanes = e->trace_on ? 1 : std::min(ngroups, MZ_ENC_LANES);
+    hipStream_t st[2] = {e->c->stream, e->ls[0]};
+    if (nlanes > 1) {
+        TRY(hipEventRecord(e->fork, st[0]), "hipEventRecord");
+        TRY(hipStreamWaitEvent(st[1], e->fork, 0), "hipStreamWaitEvent");
+    }
+    for (int g0 = 0, gi = 0; g0 < n; g0 += e->eg, gi++) {
+        const int gn = std::min(e->eg, n - g0), k = gi % nlanes;
+        if (int r = encode_impl(e, mels + (size_t)g0 * nm * NFR, on_device, gn, g0, k, st[k], e->xkvbuf)) return r;
+    }
+    if (nlanes > 1) {
+        TRY(hipEventRecord(e->join[0], st[1]), "hipEventRecord");
+        TRY(hipStreamWaitEvent(st[0], e->join[0], 0), "hipStreamWaitEvent");
+    }
+    TRY(hipEventRecord(e->enc_done, st[0]), "hipEventRecord");
+    e->pending_n = n;
+    e->pending_enq = since(t0);
+    return MZ_OK;
+}
+
+static int check_frames(const int32_t* frames, int n, const char* who) {
     for (int c = 0; c < n; c++)
         if (frames[c] < 0 || frames[c] > NFR)
-            return mz_fail(MZ_ERR_ARG, "mz_transcribe: clip %d has %d frames (0..%d)", c, frames[c], NFR);
-    const int mt = e->dm.max_t, nm = e->dm.n_mels, eos = e->eos, np = prompt_len;
-    auto sec = [](clk::time_point a) { return std::chrono::duration<double>(clk::now() - a).count(); };
+            return mz_fail(MZ_ERR_ARG, "%s: clip %d has %d frames (0..%d)", who, c, frames[c], NFR);
+    return MZ_OK;
+}
+
+// Decodes the oldest submitted chunk and computes its token timestamps (the rest of transcribe,
+// src/transcribe.rs:118-167). times->enc is the host's enqueue time at submission plus its wait here for the encoder.
+static int collect_impl(mz_engine* e, const int32_t* frames, int n, const int32_t* prompt, int prompt_len, int detect,
+                        int use_graph, int max_new, int half_align, int32_t* seq, int32_t* seq_len, float* ts,
+                        int32_t* langs, mz_times* times) {
+    if (!e || !frames || !prompt || !seq || !seq_len || !ts || !langs)
+        return mz_fail(MZ_ERR_ARG, "mz_transcribe_collect: null argument");
+    if (!e->pending_n) return mz_fail(MZ_ERR_STATE, "mz_transcribe_collect: no chunk submitted");
+    if (n != e->pending_n)
+        return mz_fail(MZ_ERR_ARG, "mz_transcribe_collect: %d clips, the submitted chunk has %d", n, e->pending_n);
+    if (prompt_len <= 0 || prompt_len >= e->dm.max_t)
+        return mz_fail(MZ_ERR_ARG, "mz_transcribe_collect: prompt of %d", prompt_len);
+    if (int r = check_frames(frames, n, "mz_transcribe_collect")) return r;
+    e->pending_n = 0;
+    const int mt = e->dm.max_t, eos = e->eos, np = prompt_len;
+    auto sec = since;
     mz_times tm{};
 
     auto t0 = clk::now();
-    // groups go round-robin over the encoder lanes (the extra lanes wait for the caller's work on the main stream,
-    // the main stream for them before decoding)
-    const int ngroups = (n + e->eg - 1) / e->eg;
-    const int nlanes = e->trace_on ? 1 : std::min(ngroups, MZ_ENC_LANES);
-    if (nlanes > 1) TRY(hipEventRecord(e->fork, e->c->stream), "hipEventRecord");
-    for (int k = 1; k < nlanes; k++) TRY(hipStreamWaitEvent(e->ls[k - 1], e->fork, 0), "hipStreamWaitEvent");
-    for (int g0 = 0, gi = 0; g0 < n; g0 += e->eg, gi++) {
-        const int gn = std::min(e->eg, n - g0);
-        if (int r = encode_impl(e, mels + (size_t)g0 * nm * NFR, on_device, gn, g0, gi % nlanes)) return r;
-    }
-    for (int k = 1; k < nlanes; k++) {
-        TRY(hipEventRecord(e->join[k - 1], e->ls[k - 1]), "hipEventRecord");
-        TRY(hipStreamWaitEvent(e->c->stream, e->join[k - 1], 0), "hipStreamWaitEvent");
-    }
-    if (int r = mz_sync(e->c)) return r;
-    tm.enc = sec(t0);
+    TRY(hipEventSynchronize(e->enc_done), "encoder wait");
+    tm.enc = e->pending_enq + sec(t0);
 
     t0 = clk::now();
     std::vector<int32_t> pr((size_t)n * np);
@@ -1116,6 +1160,37 @@ static int transcribe_impl(mz_engine* e, const float* mels, bool on_device, cons
     tm.post = sec(t0);
     if (times) *times = tm;
     return MZ_OK;
+}
+
+static int transcribe_impl(mz_engine* e, const float* mels, bool on_device, const int32_t* frames, int n,
+                           const int32_t* prompt, int prompt_len, int detect, int use_graph, int max_new,
+                           int half_align, int32_t* seq, int32_t* seq_len, float* ts, int32_t* langs,
+                           mz_times* times) {
+    if (!e || !mels || !frames || !prompt || !seq || !seq_len || !ts || !langs)
+        return mz_fail(MZ_ERR_ARG, "mz_transcribe: null argument");
+    if (e->pending_n) return mz_fail(MZ_ERR_STATE, "mz_transcribe: a submitted chunk is not collected");
+    if (n <= 0 || n > e->bmax) return mz_fail(MZ_ERR_ARG, "mz_transcribe: %d clips (bmax %d)", n, e->bmax);
+    if (prompt_len <= 0 || prompt_len >= e->dm.max_t)
+        return mz_fail(MZ_ERR_ARG, "mz_transcribe: prompt of %d", prompt_len);
+    if (int r = check_frames(frames, n, "mz_transcribe")) return r;
+    if (int r = submit_impl(e, mels, on_device, n)) return r;
+    return collect_impl(e, frames, n, prompt, prompt_len, detect, use_graph, max_new, half_align, seq, seq_len, ts,
+                        langs, times);
+}
+
+extern "C" int mz_transcribe_submit(mz_engine* e, const float* mels, int n) {
+    return submit_impl(e, mels, false, n);
+}
+
+extern "C" int mz_transcribe_submit_device(mz_engine* e, uint64_t mels, int n) {
+    return submit_impl(e, (const float*)(uintptr_t)mels, true, n);
+}
+
+extern "C" int mz_transcribe_collect(mz_engine* e, const int32_t* frames, int n, const int32_t* prompt,
+                                     int prompt_len, int detect, int use_graph, int max_new, int half_align,
+                                     int32_t* seq, int32_t* seq_len, float* ts, int32_t* langs, mz_times* times) {
+    return collect_impl(e, frames, n, prompt, prompt_len, detect, use_graph, max_new, half_align, seq, seq_len, ts,
+                        langs, times);
 }
 
 extern "C" int mz_transcribe(mz_engine* e, const float* mels, const int32_t* frames, int n, const int32_t* prompt,

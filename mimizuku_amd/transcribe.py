@@ -70,16 +70,27 @@ def transcribe(e: Engine, mels, p: Prompt, frames=None, graph: bool = True, max_
     max_new > 0 caps the generated tokens (the reference decodes until every row ends or max_t - 1 steps).
     half_align rounds the timestamp arithmetic through fp16 where an fp16 model does (src/align.rs).
     """
-    on_device = isinstance(mels, int)
-    if on_device:
+    m, n = _mels(e, mels, n)
+    return _decode(e, n, p, frames, graph, max_new, half_align,
+                   lambda args: L.lib().mz_transcribe_device(e.h, m, *args) if isinstance(m, int)
+                   else L.lib().mz_transcribe(e.h, ptr(m), *args))
+
+
+def _mels(e: Engine, mels, n):
+    if isinstance(mels, int):
         if n is None:
             raise MzError("transcribe: the clip count n is needed with device-resident mels")
-    else:
-        m = np.ascontiguousarray(mels, np.float32)
-        n = m.shape[0]
-        if m.shape[1:] != (e.dims.n_mels, NFRAMES):
-            raise MzError(f"mels must be [n][{e.dims.n_mels}][{NFRAMES}], got {m.shape}")
+        return mels, n
+    m = np.ascontiguousarray(mels, np.float32)
+    if m.ndim != 3 or m.shape[1:] != (e.dims.n_mels, NFRAMES):
+        raise MzError(f"mels must be [n][{e.dims.n_mels}][{NFRAMES}], got {m.shape}")
+    return m, m.shape[0]
+
+
+def _decode(e: Engine, n: int, p: Prompt, frames, graph, max_new, half_align, call):
     fr = np.ascontiguousarray(np.full(n, NFRAMES, np.int32) if frames is None else np.array(frames, np.int32))
+    if fr.shape != (n,):
+        raise MzError(f"frames must hold {n} counts, got {fr.shape}")
     prompt = np.array(p.tokens(p.lang if p.lang is not None else p.sot), np.int32)
     mt = e.dims.max_t
     seq = np.zeros((n, mt), np.int32)
@@ -87,14 +98,43 @@ def transcribe(e: Engine, mels, p: Prompt, frames=None, graph: bool = True, max_
     ts = np.zeros((n, mt), np.float32)
     langs = np.zeros(n, np.int32)
     tm = L.Times()
-    args = (ptr(fr), n, ptr(prompt), len(prompt), int(p.detect()), int(graph), int(max_new), int(half_align),
-            ptr(seq), ptr(seq_len), ptr(ts), ptr(langs), C.byref(tm))
-    if on_device:
-        check(L.lib().mz_transcribe_device(e.h, mels, *args))
-    else:
-        check(L.lib().mz_transcribe(e.h, ptr(m), *args))
+    check(call((ptr(fr), n, ptr(prompt), len(prompt), int(p.detect()), int(graph), int(max_new), int(half_align),
+                ptr(seq), ptr(seq_len), ptr(ts), ptr(langs), C.byref(tm))))
     out = [Decoded(int(langs[i]), seq[i, :seq_len[i]].tolist(), ts[i, :seq_len[i]].tolist()) for i in range(n)]
     return out, Times(tm.enc, tm.dec, tm.post, tm.steps)
+
+
+def submit(e: Engine, mels, n: int | None = None) -> int:
+    """Enqueue the encoder of one chunk of up to e.bmax clips and return its clip count (mz_transcribe_submit);
+    collect it before submitting another."""
+    m, n = _mels(e, mels, n)
+    check(L.lib().mz_transcribe_submit_device(e.h, m, n) if isinstance(m, int)
+          else L.lib().mz_transcribe_submit(e.h, ptr(m), n))
+    return n
+
+
+def collect(e: Engine, n: int, p: Prompt, frames=None, graph: bool = True, max_new: int = 0,
+            half_align: bool = True) -> tuple[list[Decoded], Times]:
+    """Decode the submitted chunk (n clips) and return what transcribe returns for it (mz_transcribe_collect)."""
+    return _decode(e, n, p, frames, graph, max_new, half_align,
+                   lambda args: L.lib().mz_transcribe_collect(e.h, *args))
+
+
+def transcribe_all(e: Engine, mels, p: Prompt, frames=None, graph: bool = True, max_new: int = 0,
+                   half_align: bool = True, n: int | None = None) -> tuple[list[Decoded], Times]:
+    """Any number of clips in chunks of e.bmax, in order (the loop of src/main.rs:195-200), one transcribe per
+    chunk; the stage times are summed over the chunks."""
+    m, n = _mels(e, mels, n)
+    fr = np.full(n, NFRAMES, np.int32) if frames is None else np.asarray(frames, np.int32)
+    step = e.dims.n_mels * NFRAMES
+    out, tm = [], Times()
+    for c0 in range(0, n, e.bmax):
+        cn = min(e.bmax, n - c0)
+        o, t = transcribe(e, m + 4 * c0 * step if isinstance(m, int) else m[c0:c0 + cn], p, fr[c0:c0 + cn], graph,
+                          max_new, half_align, cn)
+        out += o
+        tm = Times(tm.enc + t.enc, tm.dec + t.dec, tm.post + t.post, tm.steps + t.steps)
+    return out, tm
 
 
 def jump_times(w: np.ndarray, cols: int, width: int = 7, half: bool = True) -> np.ndarray:

@@ -205,6 +205,34 @@ def test_graph_replay_equals_eager(ctx, case):
     np.testing.assert_array_equal(x1, x2)
 
 
+def test_submit_collect_is_transcribe(ctx, case):
+    """mz_transcribe_submit + mz_transcribe_collect (the encoder half enqueued, then the decode half) return what
+    mz_transcribe returns, bit for bit; one chunk at a time, with the protocol's errors; transcribe_all over the clips
+    in chunks of one equals one call per clip."""
+    e = case.engine(ctx)
+    p = transcribe.Prompt(e.gc, "auto" if case.detect else "en")
+    with pytest.raises(L.MzError, match="no chunk submitted"):
+        transcribe.collect(e, case.n, p)
+    ref, _ = transcribe.transcribe(e, case.mel, p, max_new=12)
+    assert transcribe.submit(e, case.mel) == case.n
+    with pytest.raises(L.MzError, match="a chunk is pending"):
+        transcribe.submit(e, case.mel)
+    with pytest.raises(L.MzError, match="not collected"):
+        transcribe.transcribe(e, case.mel, p)
+    with pytest.raises(L.MzError, match="the submitted chunk has"):
+        transcribe.collect(e, case.n + 1, p)
+    got, tm = transcribe.collect(e, case.n, p, max_new=12)
+    assert [(d.lang, d.seq, d.ts) for d in got] == [(d.lang, d.seq, d.ts) for d in ref]
+    assert tm.enc > 0 and tm.steps > 0
+    e.close()
+    e = model.Engine(ctx, case.dims, case.gc, 1, 1)
+    e.load(case.W)
+    one = [transcribe.transcribe(e, case.mel[c:c + 1], p, max_new=12)[0][0] for c in range(case.n)]
+    allc, tm = transcribe.transcribe_all(e, case.mel, p, max_new=12)
+    assert [(d.lang, d.seq, d.ts) for d in allc] == [(d.lang, d.seq, d.ts) for d in one]
+    e.close()
+
+
 def test_engine_from_model_dir_equals_put(ctx, case, tmp_path):
     """Engine.new reads the directory in the library (configs, mapped safetensors, F32 -> F16 on the host) and
     places the same bits as tensors handed over one by one: identical tokens, logits and alignment rows."""
