@@ -191,6 +191,15 @@ def probe(name: str, reps: int = 5):
                                                                          g.dec_layers * 2 * nh, nh, 2)
     elif name not in ("attn", "ln"):
         raise SystemExit(f"unknown probe {name}")
+    if name == "attn":
+        # q, k, v ~ N(0, 1) per head tile of 1536 x 64 (rows 1500.. zero), q multiplied by log2(e) / 8 as the QKV
+        # product stores it, v transposed: the attention's operands as the encoder hands them over
+        t = np.zeros((EG, 3, nh, 1536, 64), np.float16)
+        t[:, :, :, :1500] = f16((EG, 3, nh, 1500, 64))
+        t[:, 0] = (t[:, 0].astype(np.float32) * (1.4426950408889634 / 8)).astype(np.float16)
+        t[:, 2] = np.ascontiguousarray(t[:, 2].transpose(0, 1, 3, 2)).reshape(EG, nh, 1536, 64)
+        ctx.upload(heads, t)
+        del t
     lw, lb = ctx.upload_new(np.ones(d, np.float16)), ctx.upload_new(np.zeros(d, np.float16))
     for _ in range(reps):
         if name == "attn":
