@@ -149,7 +149,7 @@ struct mz_engine {
     // decoder state (bmax rows)
     f16* xkvbuf = nullptr;
     int *tok = nullptr, *done = nullptr, *ctr = nullptr;
-    float *x = nullptr, *q = nullptr, *part = nullptr, *logits = nullptr;
+    float *x = nullptr, *part = nullptr, *logits = nullptr;
     f16 *h = nullptr, *datt = nullptr, *dff = nullptr, *kc = nullptr, *vc = nullptr;
     float* align = nullptr;  // alignment-head probabilities [bmax][max_t][na][1500], fp32
     int2* amax = nullptr;  // LM head argmax partials [mz_lm_blocks(vocab)][bmax]
@@ -243,7 +243,7 @@ extern "C" size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int 
     const size_t B = bmax, G = eg;
     size_t enc = G * d->n_mels * NFR * 4 + G * NFR * d->n_mels * 2 + G * NFR * D * 2 + G * TENC * D * 4 +
                  G * TENC * D * 2 * 3 + G * 3 * nh * TPAD * HD * 2 + G * TENC * F * 2;
-    size_t dec = B * nl * 2 * nh * TPAD * HD * 2 + B * mt * 4 + B * 4 + 16 + B * D * 4 * 2 + B * D * 2 * 2 + B * F * 2 +
+    size_t dec = B * nl * 2 * nh * TPAD * HD * 2 + B * mt * 4 + B * 4 + 16 + B * D * 4 + B * D * 2 * 2 + B * F * 2 +
                  2 * nl * B * nh * mt * HD * 2 + B * V * 4 + B * mt * n_align * TENC * 4 + (size_t)mz_lm_blocks((int)V) * B * 8 +
                  nl * nh * 4 + 2 * V;
     size_t part = (size_t)MZ_MAX_PARTS * B * D * 4;
@@ -402,7 +402,7 @@ extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, in
     if ((r = mz_hip(hipEventCreateWithFlags(&e->enc_done, hipEventDisableTiming), "hipEventCreate"))) return fail(r);
     if ((r = e->alloc(&e->xkvbuf, xkv_elems(*d, bmax))) || (r = e->alloc(&e->tok, B * mt)) ||
         (r = e->alloc(&e->done, B)) || (r = e->alloc(&e->ctr, 4)) || (r = e->alloc(&e->x, B * D)) ||
-        (r = e->alloc(&e->q, B * D)) || (r = e->alloc(&e->h, B * D)) || (r = e->alloc(&e->datt, B * D)) ||
+        (r = e->alloc(&e->h, B * D)) || (r = e->alloc(&e->datt, B * D)) ||
         (r = e->alloc(&e->dff, B * F)) || (r = e->alloc(&e->kc, (size_t)nl * B * nh * mt * HD)) ||
         (r = e->alloc(&e->vc, (size_t)nl * B * nh * mt * HD)) || (r = e->alloc(&e->logits, B * V)) ||
         (r = e->alloc(&e->align, B * mt * e->na * (size_t)TENC)) ||
@@ -416,7 +416,8 @@ extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, in
         return fail(r);
     // split-K partials: the largest ks * rows * n over the decoder products
     size_t pe = 0;
-    for (auto nk : {std::pair<int, int>{D, D}, {D, F}}) pe = std::max(pe, (size_t)ksplit_for(nk.first, nk.second) * B * nk.first);
+    for (auto nk : {std::pair<int, int>{D, D}, {D, F}, {3 * D, D}})
+        pe = std::max(pe, (size_t)ksplit_for(nk.first, nk.second) * B * nk.first);
     e->part_elems = pe;
     if ((r = e->alloc(&e->part, pe))) return fail(r);
 
@@ -762,8 +763,8 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
         g.ctr = e->ctr;
         return mz_dec_gemm_launch(s, epi, g);
     };
-    auto attn = [&](const float* q, int nq, const f16* wq, const f16* qbias, const f16* k, const f16* v, long kv_b,
-                    int L, const int* aslot) {
+    auto attn_args = [&](const float* q, int nq, const f16* wq, const f16* qbias, const f16* k, const f16* v, long kv_b,
+                         int L, const int* aslot) {
         MzDecAttn a{};
         a.q = q;
         a.nq = nq;
@@ -786,34 +787,30 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
         a.aslot = aslot;
         a.align = e->align;
         a.na = e->na;
-        return mz_dec_attn_launch(s, a);
+        return a;
     };
-    const int ks_dd = ksplit_for(D, D), ks_df = ksplit_for(D, F);
+    auto attn = [&](const float* q, int nq, const f16* wq, const f16* qbias, const f16* k, const f16* v, long kv_b,
+                    int L, const int* aslot) {
+        return mz_dec_attn_launch(s, attn_args(q, nq, wq, qbias, k, v, kv_b, L, aslot));
+    };
+    const int ks_dd = ksplit_for(D, D), ks_df = ksplit_for(D, F), ks_qkv = ksplit_for(3 * D, D);
     const f16* xkv = e->xkvbuf;
     for (int i = 0; i < nl; i++) {
         const DecLayer& L = e->decv[i];
         f16* kc = e->kc + (size_t)i * e->bmax * nh * mt * HD;
         f16* vc = e->vc + (size_t)i * e->bmax * nh * mt * HD;
+        // q/k/v as split-K partials; the self-attention sums them for its (row, head), adds the bias and writes the
+        // step's key and value into the cache
+        PROF(MZ_K_DEC_QKV, gemm(DEPI_PARTIAL, e->h, D, L.qkv, 3 * D, D, ks_qkv, e->part, 3 * D), "dec qkv");
         {
-            MzDec g{};
-            g.x = e->h;
-            g.ldx = D;
-            g.W = L.qkv.w;
-            g.bias = L.qkv.b;
-            g.M = b;
-            g.N = 3 * D;
-            g.K = D;
-            g.ksplit = 1;
-            g.out = e->q;
-            g.ldo = D;
-            g.kc = kc;
-            g.vc = vc;
-            g.ctr = e->ctr;
-            g.maxT = mt;
-            g.d = D;
-            PROF(MZ_K_DEC_QKV, mz_dec_gemm_launch(s, DEPI_QKV, g), "dec qkv");
+            MzDecAttn a = attn_args(e->part, ks_qkv, nullptr, L.qkv.b, kc, vc, (long)nh * mt * HD, -1, nullptr);
+            a.qstride = (long)b * 3 * D;
+            a.qrow = 3 * D;
+            a.kw = kc;
+            a.vw = vc;
+            a.kvbias = L.qkv.b + D;
+            PROF(MZ_K_DEC_SELF, mz_dec_attn_launch(s, a), "self attention");
         }
-        PROF(MZ_K_DEC_SELF, attn(e->q, 1, nullptr, nullptr, kc, vc, (long)nh * mt * HD, -1, nullptr), "self attention");
         PROF(MZ_K_DEC_OPROJ, gemm(DEPI_PARTIAL, e->datt, D, L.o, D, D, ks_dd, e->part, D), "dec out-proj");
         PROF(MZ_K_DEC_ADDLN,
              mz_dec_add_ln_launch(s, e->x, e->part, ks_dd, (long)b * D, L.o.b, L.lnx.w, L.lnx.b, e->h, b, D, EPS),
@@ -990,7 +987,7 @@ extern "C" int mz_engine_free(mz_engine* e) {
         if (p) mz_free(e->c, (uint64_t)(uintptr_t)p);
     for (void* p : {(void*)e->arena, (void*)e->mel, (void*)e->melT, (void*)e->h1, (void*)e->ex, (void*)e->hb, (void*)e->dd,
                     (void*)e->qkvh, (void*)e->att, (void*)e->ff, (void*)e->trace, (void*)e->dtrace, (void*)e->xkvbuf, (void*)e->tok,
-                    (void*)e->done, (void*)e->ctr, (void*)e->x, (void*)e->q, (void*)e->h, (void*)e->datt,
+                    (void*)e->done, (void*)e->ctr, (void*)e->x, (void*)e->h, (void*)e->datt,
                     (void*)e->dff, (void*)e->kc, (void*)e->vc, (void*)e->logits, (void*)e->align, (void*)e->amax,
                     (void*)e->aslot, (void*)e->sup, (void*)e->sup_lang,
                     (void*)e->part})

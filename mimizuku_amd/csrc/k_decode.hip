@@ -13,12 +13,13 @@
 //   dec_gemm      skinny GEMM for M <= 32 rows per tile on the matrix cores: both operands of a K slice loaded
 //                 straight into LDS at once, W rows the 32x32x16 MFMA A operand and x rows the B operand; split-K
 //                 over workgroups (grid.y) and over the 4 waves of a workgroup. Epilogues: fp32 split-K partials,
-//                 GELU -> fp16, fp16, the self-attention q/k/v scatter into the cache, or logits with a masked
-//                 per-workgroup argmax (gemv_* + cuBLAS + fill_bias + kv_write, whisper.cu:92-97, 309-317, 497-567)
-//   dec_attn      attention of one query per (row, head) over a run of keys: self-attention over the cache
-//                 (whisper.cu:319-353) and cross-attention over the encoder keys/values, which projects its own
-//                 query from the row's LayerNorm output and records the alignment-head probabilities
-//                 (whisper.cu:355-449)
+//                 GELU -> fp16, fp16, or logits with a masked per-workgroup argmax (gemv_* + cuBLAS + fill_bias,
+//                 whisper.cu:92-97, 309-317, 497-567)
+//   dec_attn      attention of one query per (row, head) over a run of keys: self-attention over the cache, which
+//                 sums the q/k/v projection's split-K partials for its (row, head), adds the bias and writes the
+//                 step's key and value into the cache (kv_write + whisper.cu:319-353), and cross-attention over the
+//                 encoder keys/values, which projects its own query from the row's LayerNorm output and records the
+//                 alignment-head probabilities (whisper.cu:355-449)
 //   dec_add_ln    residual add of the split-K partials + bias, fused with the next LayerNorm (whisper.cu:71-82)
 //   dec_argmax    greedy choice from the per-workgroup argmax partials; advances the position (whisper.cu:451-495)
 #include "mz_common.h"
@@ -171,7 +172,7 @@ __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
         bv[e] = (EPI != DEPI_PARTIAL && p.bias) ? (float)p.bias[n] : 0.f;
         msk[e] = EPI == DEPI_LOGITS ? p.sup[n] != 0 : false;
     }
-    const int pos = (EPI == DEPI_LOGITS || EPI == DEPI_QKV) ? p.ctr[1] : 0;
+    const int pos = EPI == DEPI_LOGITS ? p.ctr[1] : 0;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
@@ -238,15 +239,6 @@ __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
             ((f16*)p.out)[(long)m * p.ldo + n] = (f16)gelu_erf(a);
         } else if (EPI == DEPI_F16) {
             ((f16*)p.out)[(long)m * p.ldo + n] = (f16)a;
-        } else if (EPI == DEPI_QKV) {
-            // q -> fp32 [m][d]; k and v -> the cache rows [m][head][pos][64] (not stored outside the cache)
-            const int which = n / p.d, c = n - which * p.d, head = c >> 6, dim = c & 63, nh = p.d >> 6;
-            if (which == 0) {
-                ((float*)p.out)[(long)m * p.d + c] = a;
-            } else if (pos < p.maxT) {
-                f16* dst = which == 1 ? p.kc : p.vc;
-                dst[(((long)m * nh + head) * p.maxT + pos) * MZ_HD + dim] = (f16)a;
-            }
         }
     }
 #endif
@@ -413,6 +405,7 @@ __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
     __shared__ float gm[AG], gl[AG];
     __shared__ float gacc[AG][MZ_HD + 1];
     __shared__ float tot[2];
+    __shared__ __attribute__((aligned(16))) f16 kvn[2][MZ_HD];  // the step's own key and value (self, kw set)
 
     const int bh = blockIdx.x, b = bh / a.nh, head = bh - b * a.nh;
     if (a.done[b]) return;
@@ -473,13 +466,26 @@ __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
         }
     } else {
         fetch(grp);
-        if (tid < MZ_HD) {
-            float q = a.qbias ? (float)a.qbias[head * MZ_HD + tid] : 0.f;
-            for (int s = 0; s < a.nq; s++) q += a.q[s * a.qstride + (long)b * a.d + head * MZ_HD + tid];
-            qs[tid] = q * QS;
+        // thread 64 w + i takes dim i of q (w = 0) or, with kw set, of the step's key (1) or value (2)
+        const long qrow = a.qrow ? a.qrow : a.d;
+        if (tid < ((!CROSS && a.kw) ? 3 : 1) * MZ_HD) {
+            const int which = tid >> 6, i = tid & 63, col = which * a.d + head * MZ_HD + i;
+            const f16* bias = which == 0 ? a.qbias : a.kvbias ? a.kvbias + (which - 1) * a.d : nullptr;
+            float v = bias ? (float)bias[head * MZ_HD + i] : 0.f;
+            for (int s = 0; s < a.nq; s++) v += a.q[s * a.qstride + (long)b * qrow + col];
+            if (which == 0) {
+                qs[i] = v * QS;
+            } else {
+                const f16 h = (f16)v;
+                kvn[which - 1][i] = h;
+                if (pos < a.maxT)
+                    (which == 1 ? a.kw : a.vw)[(long)b * a.kv_b + (long)head * a.kv_h + (long)pos * MZ_HD + i] = h;
+            }
         }
     }
     __syncthreads();
+    // with kw set the step's position is read from kvn, never from the cache this workgroup has just written
+    const bool own = !CROSS && a.kw != nullptr;
     float q8[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) q8[e] = qs[sub * 8 + e];
@@ -487,6 +493,14 @@ __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
     float m = -INFINITY, l = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int j0 = grp; j0 < L; j0 += AG * AU) {
         if (j0 != grp) fetch(j0);
+        if (own) {
+#pragma unroll
+            for (int u = 0; u < AU; u++)
+                if (j0 + u * AG == pos) {
+                    kk[u] = *(const f16x8*)&kvn[0][sub * 8];
+                    vv[u] = *(const f16x8*)&kvn[1][sub * 8];
+                }
+        }
         float s[AU];
 #pragma unroll
         for (int u = 0; u < AU; u++) {
@@ -609,7 +623,6 @@ hipError_t mz_dec_gemm_launch(hipStream_t s, int epi, const MzDec& g) {
     if (g.K % 64 != 0 || g.M <= 0 || g.N <= 0 || g.ksplit <= 0 || (g.K / 64) % g.ksplit != 0 ||
         g.K / g.ksplit > MZ_DEC_KSLICE || g.ldx % 8 != 0)
         return hipErrorInvalidValue;
-    if (epi == DEPI_QKV && (g.N != 3 * g.d || g.d % 64 != 0 || !g.kc || !g.vc || !g.ctr)) return hipErrorInvalidValue;
     if (epi == DEPI_LOGITS && (!g.sup || !g.amax || !g.ctr || g.N > 65536 || g.K > MZ_DEC_KSLICE)) return hipErrorInvalidValue;
     if (epi != DEPI_PARTIAL && g.ksplit != 1) return hipErrorInvalidValue;
     const dim3 grid((g.N + 31) / 32, g.ksplit, (g.M + 31) / 32);
@@ -618,13 +631,13 @@ hipError_t mz_dec_gemm_launch(hipStream_t s, int epi, const MzDec& g) {
         case DEPI_PARTIAL:
             if (ksl <= 256) hipLaunchKernelGGL((dec_gemm_kernel<DEPI_PARTIAL, 256>), grid, dim3(256), 0, s, g);
             else if (ksl <= 512) hipLaunchKernelGGL((dec_gemm_kernel<DEPI_PARTIAL, 512>), grid, dim3(256), 0, s, g);
+            else if (ksl <= 640) hipLaunchKernelGGL((dec_gemm_kernel<DEPI_PARTIAL, 640>), grid, dim3(256), 0, s, g);
             else if (ksl <= 1024) hipLaunchKernelGGL((dec_gemm_kernel<DEPI_PARTIAL, 1024>), grid, dim3(256), 0, s, g);
             else hipLaunchKernelGGL((dec_gemm_kernel<DEPI_PARTIAL, MZ_DEC_KSLICE>), grid, dim3(256), 0, s, g);
             break;
         case DEPI_GELU_F16:
             hipLaunchKernelGGL((dec_gemm_kernel<DEPI_GELU_F16, MZ_DEC_KSLICE>), grid, dim3(256), 0, s, g);
             break;
-        case DEPI_QKV: hipLaunchKernelGGL((dec_gemm_kernel<DEPI_QKV, MZ_DEC_KSLICE>), grid, dim3(256), 0, s, g); break;
         case DEPI_F16: hipLaunchKernelGGL((dec_gemm_kernel<DEPI_F16, MZ_DEC_KSLICE>), grid, dim3(256), 0, s, g); break;
         case DEPI_LOGITS: {
             const int T = mz_lm_tiles_per_block(g.N);

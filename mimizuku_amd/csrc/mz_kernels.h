@@ -67,7 +67,6 @@ enum MzDecEpi {
     DEPI_GELU_F16 = 1, // out f16 [m][ldo] = gelu(acc + bias)
     DEPI_LOGITS = 2,   // out f32 [m][ldo] = acc, and amax[wg][m] = masked (max, lowest id) of each workgroup's ids
                        // (mz_lm_blocks(N) workgroups per 32-row block; K <= MZ_DEC_KSLICE)
-    DEPI_QKV = 3,      // q -> out f32 [m][d] (+bias); k, v (+bias) -> self cache rows at position ctr[1]
     DEPI_F16 = 4,      // out f16 [m][ldo] = acc + bias
 };
 struct MzDec {
@@ -79,10 +78,6 @@ struct MzDec {
     void* out;
     long ldo;
     const int* ctr;
-    // DEPI_QKV: this layer's cache, [bmax][nh][maxT][64] for both k and v
-    f16* kc;
-    f16* vc;
-    int maxT, d;
     // DEPI_LOGITS: mask (nonzero = never chosen), begin-suppressed ids at the first generated position, partials
     const unsigned char* sup;
     int bs1, bs2, prompt_len;
@@ -94,12 +89,19 @@ int mz_lm_blocks(int N);
 int mz_lm_tiles_per_block(int N);
 
 struct MzDecAttn {
-    // query: sum over nq slices of q[s * qstride + b * d + head * 64 + i] (+ qbias), scaled by 1/8; or, when wq is
-    // set, the projection xin[b] . wq[head * 64 + i] (+ qbias) computed in the kernel (d <= MZ_DEC_KSLICE)
+    // query: sum over nq slices of q[s * qstride + b * qrow + head * 64 + i] (+ qbias), scaled by 1/8 (qrow 0: d);
+    // or, when wq is set, the projection xin[b] . wq[head * 64 + i] (+ qbias) computed in the kernel
+    // (d <= MZ_DEC_KSLICE)
     const float* q;
     int nq;
-    long qstride;
+    long qstride, qrow;
     const f16* qbias;
+    // self-attention only, when kw is set: the slices also hold the step's key and value at columns d + head * 64 + i
+    // and 2d + head * 64 + i of each row; summed with kvbias (k then v, [2d]), rounded to fp16, they are written to
+    // the caches kw / vw (laid out as k / v) at the step's position and stand in for that position's key and value
+    f16* kw;
+    f16* vw;
+    const f16* kvbias;
     const f16* xin;  // [B][d]
     const f16* wq;   // [d][d], row = output feature
     // keys and values of (b, head): rows of 64 halves at k + b * kv_b + head * kv_h (v likewise)
