@@ -1131,7 +1131,7 @@ static int collect_impl(mz_engine* e, const int32_t* frames, int n, const int32_
         p.cost = e->ts_cost;
         p.trace = e->ts_trace;
         p.diag_stride = mz_ts_diag_stride(rmax, TENC);
-        p.ldd = rmax + 1;
+        p.ldd = mz_ts_ldd(rmax);
         p.out = e->ts_out;
         p.out_stride = mt;
         TRY(mz_ts_launch(e->c->stream, p, n), "timestamp kernels");

@@ -239,6 +239,130 @@ __global__ void __launch_bounds__(1024) ts_dtw_kernel(const MzTs p) {
 #endif
 }
 
+// Tables of at most 256 rows (R <= 255): one wave per clip. Lane l holds table rows 4l .. 4l + 3 of the two
+// previous anti-diagonals in registers and takes row 4l - 1 from lane l - 1 through cross-lane moves, so a diagonal
+// needs no barrier and no LDS round trip; its costs arrive four per lane, one 16-byte load per lane for the whole
+// diagonal, DTW_PF diagonals ahead. The move into each cell (2 bits) is packed into LDS ([diagonal][lane], a byte
+// per lane), where the path is walked back. Same comparisons and roundings as ts_dtw_kernel, so the same bits.
+constexpr int DTW_PF = 8;
+constexpr int DTW_WAVE_ND = 256 + 1500;  // diagonals held in LDS: rows 0 .. 255, columns 0 .. 1500
+
+// lane l gets lane l - 1's v (lane 0: 0): a row shift within each 16-lane row (DPP row_shr:1), and the first lane of
+// rows 1 .. 3 takes the last lane of the row before through lane reads
+__device__ __forceinline__ float lane_prev(float v, int lane) {
+    const int x = __builtin_bit_cast(int, v);
+    int y = __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);
+    const int x15 = __builtin_amdgcn_readlane(x, 15), x31 = __builtin_amdgcn_readlane(x, 31),
+              x47 = __builtin_amdgcn_readlane(x, 47);
+    y = lane == 16 ? x15 : lane == 32 ? x31 : lane == 48 ? x47 : y;
+    return __builtin_bit_cast(float, y);
+}
+
+__global__ void __launch_bounds__(64) ts_dtw_wave_kernel(const MzTs p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __shared__ unsigned char moves[DTW_WAVE_ND * 64];  // [diagonal][lane]
+    __shared__ int first[257];                         // per row; [R + 1]: the first token row's offset
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const int c = blockIdx.x, R = p.rc[c].x, C = p.rc[c].y, lane = threadIdx.x;
+    float* out = p.out + (long)c * p.out_stride;
+    if (R <= 0) return;
+    if (C <= 0) {
+        for (int k = lane; k < R; k += 64) out[k] = 0.f;
+        return;
+    }
+    const int ld = p.ldd, nd = R + C + 1;
+    // reads past the clip's cost table return zeros (the descriptor's range check); rows past R are never used
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.cost + c * p.diag_stride), (short)0, (int)(p.diag_stride * 4), 0x00020000);
+    auto load = [&](int d) {
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, (unsigned)((d * ld + 4 * lane) * 4),
+                                                                                0, 0));
+    };
+    u32x4 ring[DTW_PF];
+#pragma unroll
+    for (int k = 0; k < DTW_PF; k++) ring[k] = load(k);
+    float D1[4], D2[4];  // diagonals d - 1 and d - 2 of rows 4 lane + r
+#pragma unroll
+    for (int r = 0; r < 4; r++) D1[r] = D2[r] = INFINITY;
+    for (int d0 = 0; d0 < nd; d0 += DTW_PF) {
+#pragma unroll
+        for (int k = 0; k < DTW_PF; k++) {
+            const int d = d0 + k;
+            if (d >= nd) break;
+            const u32x4 cw = ring[k];
+            ring[k] = load(d + DTW_PF);
+            const float up1 = lane_prev(D1[3], lane), up2 = lane_prev(D2[3], lane);  // row 4 lane - 1 (lane 0: unused)
+            const int lo = max(0, d - C), hi = min(R, d);
+            float nv[4];
+            unsigned bits = 0;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int i = 4 * lane + r, j = d - i;
+                const float c0 = r ? D2[r - 1] : up2, c1 = r ? D1[r - 1] : up1, c2 = D1[r];
+                float v;
+                unsigned t;
+                if (i == 0) {
+                    v = d == 0 ? 0.f : INFINITY;
+                    t = 2;
+                } else if (j == 0) {
+                    v = INFINITY;
+                    t = 1;
+                } else {
+                    float m;
+                    if (c0 < c1 && c0 < c2) {
+                        m = c0;
+                        t = 0;
+                    } else if (c1 < c0 && c1 < c2) {
+                        m = c1;
+                        t = 1;
+                    } else {
+                        m = c2;
+                        t = 2;
+                    }
+                    v = (float)(-(double)__uint_as_float(cw[r]) + (double)m);
+                }
+                const bool ok = i >= lo && i <= hi;
+                nv[r] = ok ? v : D1[r];
+                bits |= (ok ? t : 0u) << (2 * r);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                D2[r] = D1[r];
+                D1[r] = nv[r];
+            }
+            moves[d * 64 + lane] = (unsigned char)bits;
+        }
+    }
+    __syncthreads();
+    if (lane == 0) {
+        // at most R + C moves from (R, C) to (0, 0); row 0 moves left and column 0 up, as the table's edges do
+        int i = R, j = C;
+        bool row0 = false;
+        for (int n = 0; n < R + C && (i > 0 || j > 0); n++) {
+            first[i] = j - 1;
+            row0 |= i == 0;
+            unsigned t = (moves[(i + j) * 64 + (i >> 2)] >> (2 * (i & 3))) & 3u;
+            if (i == 0) t = 2;
+            else if (j == 0) t = 1;
+            if (t == 0) {
+                i--;
+                j--;
+            } else if (t == 1) {
+                i--;
+            } else {
+                j--;
+            }
+        }
+        // the token rows start at text index -1 when the path ran along row 0, else at 0
+        first[R + 1] = row0 ? 0 : 1;
+    }
+    __syncthreads();
+    const int r0 = first[R + 1];  // one start per row
+#pragma unroll 1
+    for (int n = lane; n < R; n += 64) out[n] = (float)((double)first[r0 + n] * 0.02);
+#endif
+}
+
 }  // namespace
 
 // 3 diagonals, the first-column table and 2 chunks of DTW_CH diagonals of costs, ld = rmax + 1 floats each
@@ -257,6 +381,11 @@ hipError_t mz_ts_launch(hipStream_t s, const MzTs& p, int n) {
             hipLaunchKernelGGL(ts_cost_kernel<7>, gc, dim3(256), 0, s, p);
         else
             hipLaunchKernelGGL(ts_cost_kernel<0>, gc, dim3(256), 0, s, p);
+    }
+    // the wave kernel loads rows 4 lane .. 4 lane + 3 of a diagonal as one aligned 16-byte group: ldd % 4 == 0
+    if (p.rmax <= 255 && p.ldd % 4 == 0 && p.rmax + p.cols_full + 1 <= DTW_WAVE_ND && p.diag_stride * 4 < (1L << 31)) {
+        hipLaunchKernelGGL(ts_dtw_wave_kernel, dim3(n), dim3(64), 0, s, p);
+        return hipGetLastError();
     }
     int nt = ((p.rmax + 1 + 63) / 64) * 64;
     nt = nt < 256 ? 256 : nt > 1024 ? 1024 : nt;
@@ -353,7 +482,7 @@ extern "C" int mz_jump_times_device_noalloc(mz_ctx* c, uint64_t w, int64_t clip_
         p.cost = (float*)carve((size_t)k * ds * 5);
         p.trace = (signed char*)(p.cost + (size_t)k * ds);
         p.diag_stride = ds;
-        p.ldd = rmax + 1;
+        p.ldd = mz_ts_ldd(rmax);
         p.out = (float*)carve((size_t)k * out_stride * 4);
         p.out_stride = out_stride;
         int r = mz_hip(hipMemcpyAsync((void*)p.rc, rc, (size_t)k * sizeof(int2), hipMemcpyHostToDevice, c->stream),

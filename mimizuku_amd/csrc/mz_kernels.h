@@ -134,7 +134,7 @@ hipError_t mz_dec_argmax_launch(hipStream_t s, const int2* amax, int nblk, int* 
 // ---------------------------------------------------------------- token timestamps
 // Alignment rows of clip c: w + c * clip_stride floats, rc[c].x rows of heads x cols_full floats, of which the first
 // rc[c].y columns are used. Scratch per clip: mean and sd [heads][cols_full]; cost (f32) and trace (i8) in
-// anti-diagonal-major order [rmax + cols_full + 1][ldd], ldd >= rmax + 1, diag_stride elements apart.
+// anti-diagonal-major order [rmax + cols_full + 1][ldd], ldd = mz_ts_ldd(rmax), diag_stride elements apart.
 #define MZ_TS_MAX_WIDTH 15
 struct MzTs {
     const float* w;
@@ -150,8 +150,11 @@ struct MzTs {
     float* out;  // out[c * out_stride + k], k < rc[c].x: start time in seconds of row k's token
     long out_stride;
 };
+// floats per diagonal: rows 0 .. rmax rounded up to a multiple of 4, so every diagonal starts 16-byte aligned and a
+// 4-row group never straddles two diagonals
+inline int mz_ts_ldd(int rmax) { return (rmax + 4) & ~3; }
 // scratch elements per clip for cost / trace
-inline long mz_ts_diag_stride(int rmax, int cols_full) { return (long)(rmax + cols_full + 1) * (rmax + 1); }
+inline long mz_ts_diag_stride(int rmax, int cols_full) { return (long)(rmax + cols_full + 1) * mz_ts_ldd(rmax); }
 hipError_t mz_ts_launch(hipStream_t s, const MzTs& p, int n);
 // the static scratch of mz_jump_times_device_noalloc (64 MiB per device) and the clips it takes per pass
 #define MZ_TS_SCRATCH_BYTES (64u << 20)

@@ -338,7 +338,7 @@ extern "C" int mz_jump_times_device(mz_ctx* c, uint64_t w, int64_t clip_stride, 
     p.cost = (float*)buf[3];
     p.trace = (signed char*)((float*)buf[3] + (size_t)n * ds);
     p.diag_stride = ds;
-    p.ldd = rmax + 1;
+    p.ldd = mz_ts_ldd(rmax);
     p.out = (float*)buf[4];
     p.out_stride = out_stride;
     int r = mz_hip(hipMemcpyAsync(buf[0], rc.data(), bytes[0], hipMemcpyHostToDevice, c->stream), "upload");

@@ -397,6 +397,21 @@ def test_timestamps_device_match_host_bits(ctx, half):
             np.testing.assert_array_equal(got[c], R.jump_times(w[c, :rows[c]], cols[c], 7, half))
 
 
+@pytest.mark.parametrize("rows,cols", [([255, 3, 128], [1500, 1500, 1]),      # one wave per clip, its largest table
+                                       ([300, 256, 9], [1500, 1499, 77])])   # more rows than a wave holds
+def test_timestamps_device_row_limits(ctx, rows, cols):
+    """Tables at and past 256 rows, where the one-wave DTW hands over to the workgroup DTW: identical floats."""
+    from mimizuku_amd import transcribe
+    rng = np.random.default_rng(sum(rows))
+    heads, full, rmax = 2, 1500, max(rows)
+    w = softmax_rows(rng, (len(rows), rmax, heads, full))
+    dw = ctx.upload_new(w)
+    got = transcribe.jump_times_device(ctx, dw, rmax * heads * full, rows, cols, heads, full, 7, True)
+    for c in range(len(rows)):
+        np.testing.assert_array_equal(got[c], transcribe.jump_times(w[c, :rows[c]], cols[c], 7, True),
+                                      err_msg=f"clip {c}")
+
+
 def test_timestamps_device_other_widths(ctx):
     from mimizuku_amd import transcribe
     rng = np.random.default_rng(5)
