@@ -243,24 +243,28 @@ __global__ void __launch_bounds__(1024) ts_dtw_kernel(const MzTs p) {
 // previous anti-diagonals in registers and takes row 4l - 1 from lane l - 1 through cross-lane moves, so a diagonal
 // needs no barrier and no LDS round trip; its costs arrive four per lane, one 16-byte load per lane for the whole
 // diagonal, DTW_PF diagonals ahead. The move into each cell (2 bits) is packed into LDS ([diagonal][lane], a byte
-// per lane), where the path is walked back. Same comparisons and roundings as ts_dtw_kernel, so the same bits.
-constexpr int DTW_PF = 8;
-constexpr int DTW_WAVE_ND = 256 + 1500;  // diagonals held in LDS: rows 0 .. 255, columns 0 .. 1500
+// per lane), where the path is walked back. Same comparisons and results as ts_dtw_kernel, so the same bits.
+constexpr int DTW_PF = 16;
+constexpr int DTW_WAVE_ND = 256 + 1500;  // diagonals of a table: rows 0 .. 255, columns 0 .. 1500
 
 // lane l gets lane l - 1's v (lane 0: 0): a row shift within each 16-lane row (DPP row_shr:1), and the first lane of
-// rows 1 .. 3 takes the last lane of the row before through lane reads
-__device__ __forceinline__ float lane_prev(float v, int lane) {
+// rows 1 .. 3 takes the last lane of the row before through lane reads merged in with per-lane bit masks (made once
+// by the caller). Bitwise merges, not selects: the compiler turns a select between lane reads into branches.
+struct LaneMasks {
+    int keep, m16, m32, m48;  // all ones where the lane keeps the row shift / is lane 16, 32, 48
+};
+__device__ __forceinline__ float lane_prev(float v, const LaneMasks& k) {
     const int x = __builtin_bit_cast(int, v);
-    int y = __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);
-    const int x15 = __builtin_amdgcn_readlane(x, 15), x31 = __builtin_amdgcn_readlane(x, 31),
-              x47 = __builtin_amdgcn_readlane(x, 47);
-    y = lane == 16 ? x15 : lane == 32 ? x31 : lane == 48 ? x47 : y;
+    int y = __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false) & k.keep;
+    y |= __builtin_amdgcn_readlane(x, 15) & k.m16;
+    y |= __builtin_amdgcn_readlane(x, 31) & k.m32;
+    y |= __builtin_amdgcn_readlane(x, 47) & k.m48;
     return __builtin_bit_cast(float, y);
 }
 
 __global__ void __launch_bounds__(64) ts_dtw_wave_kernel(const MzTs p) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    __shared__ unsigned char moves[DTW_WAVE_ND * 64];  // [diagonal][lane]
+    __shared__ unsigned char moves[(DTW_WAVE_ND + DTW_PF) * 64];  // [diagonal][lane], whole rounds of DTW_PF
     __shared__ int first[257];                         // per row; [R + 1]: the first token row's offset
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
     const int c = blockIdx.x, R = p.rc[c].x, C = p.rc[c].y, lane = threadIdx.x;
@@ -284,47 +288,39 @@ __global__ void __launch_bounds__(64) ts_dtw_wave_kernel(const MzTs p) {
     float D1[4], D2[4];  // diagonals d - 1 and d - 2 of rows 4 lane + r
 #pragma unroll
     for (int r = 0; r < 4; r++) D1[r] = D2[r] = INFINITY;
-    for (int d0 = 0; d0 < nd; d0 += DTW_PF) {
+    // Every cell of a diagonal is computed, in or out of the table: a cell outside (row past R, column past C or
+    // below 0) feeds only cells outside, and the walk back reads moves of cells inside only, forcing the edges' moves
+    // itself, so no cell needs a range test and the choice is branch free. Row 0 is 0 at (0, 0) and +inf after;
+    // column 0 (i == d) is +inf. The moves of rows 4 lane .. 4 lane + 3 pack into one byte.
+    float up2 = INFINITY;  // lane_prev of diagonal d - 2's row 4 lane + 3, carried from the diagonal before
+    const bool lane0 = lane == 0;
+    const int m16 = -(lane == 16), m32 = -(lane == 32), m48 = -(lane == 48);
+    const LaneMasks lm{~(m16 | m32 | m48), m16, m32, m48};
+    // whole rounds of DTW_PF diagonals: the ones past the table are outside cells too
+    const int ndr = (nd + DTW_PF - 1) / DTW_PF * DTW_PF;
+    for (int d0 = 0; d0 < ndr; d0 += DTW_PF) {
 #pragma unroll
         for (int k = 0; k < DTW_PF; k++) {
             const int d = d0 + k;
-            if (d >= nd) break;
             const u32x4 cw = ring[k];
             ring[k] = load(d + DTW_PF);
-            const float up1 = lane_prev(D1[3], lane), up2 = lane_prev(D2[3], lane);  // row 4 lane - 1 (lane 0: unused)
-            const int lo = max(0, d - C), hi = min(R, d);
+            const float up1 = lane_prev(D1[3], lm);  // row 4 lane - 1 at d - 1 (lane 0: unused)
             float nv[4];
             unsigned bits = 0;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int i = 4 * lane + r, j = d - i;
                 const float c0 = r ? D2[r - 1] : up2, c1 = r ? D1[r - 1] : up1, c2 = D1[r];
-                float v;
-                unsigned t;
-                if (i == 0) {
-                    v = d == 0 ? 0.f : INFINITY;
-                    t = 2;
-                } else if (j == 0) {
-                    v = INFINITY;
-                    t = 1;
-                } else {
-                    float m;
-                    if (c0 < c1 && c0 < c2) {
-                        m = c0;
-                        t = 0;
-                    } else if (c1 < c0 && c1 < c2) {
-                        m = c1;
-                        t = 1;
-                    } else {
-                        m = c2;
-                        t = 2;
-                    }
-                    v = (float)(-(double)__uint_as_float(cw[r]) + (double)m);
-                }
-                const bool ok = i >= lo && i <= hi;
-                nv[r] = ok ? v : D1[r];
-                bits |= (ok ? t : 0u) << (2 * r);
+                const bool t0 = c0 < fminf(c1, c2), t1 = c1 < fminf(c0, c2);  // no NaN among inside cells
+                const float m = t0 ? c0 : t1 ? c1 : c2;
+                // ts_dtw_kernel's fp64 -x + m rounded to fp32 equals the fp32 m - x: a sum rounded first to 53 bits
+                // and then to 24 rounds as if once, since 53 >= 2 x 24 + 2 (Figueroa, 1995)
+                float v = m - __uint_as_float(cw[r]);
+                v = 4 * lane + r == d ? INFINITY : v;
+                if (r == 0) v = lane0 ? (d == 0 ? 0.f : INFINITY) : v;
+                nv[r] = v;
+                bits |= (t0 ? 0u : t1 ? 1u : 2u) << (2 * r);
             }
+            up2 = up1;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 D2[r] = D1[r];
