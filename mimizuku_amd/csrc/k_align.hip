@@ -8,9 +8,9 @@
 //
 // Three launches per batch of clips:
 //   ts_stats_kernel  one thread per (clip, head, column): mean and population standard deviation over the rows
-//   ts_cost_kernel   one thread per (clip, row, column): median of the width-w reflect-padded window of z-scores,
-//                    summed over heads; the cell is stored in anti-diagonal-major order [d = i + j][i], so that the
-//                    DTW reads each diagonal with consecutive addresses
+//   ts_cost_kernel   one workgroup per 32 x 64 tile of (row, column): median of the width-w reflect-padded window
+//                    of z-scores, summed over heads; the cells are stored in anti-diagonal-major order
+//                    [d = i + j][i], so that the DTW reads each diagonal with consecutive addresses
 //   ts_dtw_kernel    one workgroup per clip: the DTW table is filled one anti-diagonal per step (every cell of a
 //                    diagonal depends only on the two previous diagonals, kept in LDS), the move taken into each cell
 //                    goes to a trace in the same diagonal-major order, and one lane walks the path back.
@@ -82,57 +82,86 @@ __global__ void __launch_bounds__(256) ts_stats_kernel(const MzTs p) {
     p.sd[o] = sd;
 }
 
-// W = 7: the window unrolled into registers; W = 0: any odd width up to MZ_TS_MAX_WIDTH
+// One workgroup per tile of COST_RT rows x COST_CT columns of a clip. Per head, the tile's z-scores (with the window's
+// reflect-padded halo) are computed once into LDS; each cell takes the median of its window from there, summed over
+// heads in head order. The tile's cells then leave diagonal by diagonal: the cells of one anti-diagonal within the
+// tile are consecutive rows, so each diagonal's run is one contiguous store. W = 7: the window unrolled into registers
+// (a sorting network); W = 0: any odd width up to MZ_TS_MAX_WIDTH (insertion sort).
+constexpr int COST_RT = 32, COST_CT = 64, COST_HALO = MZ_TS_MAX_WIDTH - 1;
+
 template <int W>
 __global__ void __launch_bounds__(256) ts_cost_kernel(const MzTs p) {
-    const int c = blockIdx.z, i = blockIdx.y, j = blockIdx.x * 256 + threadIdx.x;
+    __shared__ float zt[COST_RT][COST_CT + COST_HALO + 1];
+    __shared__ float val[COST_RT][COST_CT + 2];  // row stride 66: a diagonal's 32 rows fall in 32 different banks
+    const int c = blockIdx.z, i0 = blockIdx.y * COST_RT, j0 = blockIdx.x * COST_CT, tid = threadIdx.x;
     const int R = p.rc[c].x, C = p.rc[c].y;
-    if (i >= R || j >= C) return;
-    const int width = W ? W : p.width, pad = width >> 1;
-    float acc = 0.f;
+    if (i0 >= R || j0 >= C) return;
+    const int width = W ? W : p.width, pad = width >> 1, span = COST_CT + 2 * pad;
+    // the median phase: column jl = tid % 64 of rows il = tid / 64 + 4 k
+    const int jl = tid & 63, ib = tid >> 6;
+    float acc[COST_RT / 4];
+#pragma unroll
+    for (int k = 0; k < COST_RT / 4; k++) acc[k] = 0.f;
     for (int a = 0; a < p.heads; a++) {
-        const float* x = p.w + c * p.clip_stride + ((long)i * p.heads + a) * p.cols_full;
         const float* mu = p.mean + ((long)c * p.heads + a) * p.cols_full;
         const float* sd = p.sd + ((long)c * p.heads + a) * p.cols_full;
-        auto z = [&](int t) {
-            const float s = sd[t];
-            if (!(s > 0.f)) return 0.f;
-            return p.half ? rh(rh(x[t] - mu[t]) / s) : (x[t] - mu[t]) / s;
-        };
-        if (C <= pad) {
-            acc += z(j);
-            continue;
-        }
-        auto src = [&](int k) {
-            int t = j + k - pad;
+        // z of tile column cl - pad (reflected into 0 .. C - 1 as the window reads it; columns of cells past C,
+        // whose values are never stored, are clamped into range instead)
+        for (int e = tid; e < COST_RT * span; e += 256) {
+            const int il = e / span, cl = e - il * span, i = i0 + il;
+            int t = j0 + cl - pad;
             if (t < 0) t = -t;
             if (t >= C) t = 2 * (C - 1) - t;
-            return t;
-        };
-        if (W == 7) {
-            float win[7];
-#pragma unroll
-            for (int k = 0; k < 7; k++) win[k] = z(src(k));
-            acc += median7(win);
-        } else {
-            // insertion sort of the window, then its middle value
-            float win[MZ_TS_MAX_WIDTH];
-            for (int k = 0; k < width; k++) {
-                const float v = z(src(k));
-                int q = k - 1;
-                while (q >= 0 && win[q] > v) {
-                    win[q + 1] = win[q];
-                    q--;
-                }
-                win[q + 1] = v;
+            t = t < 0 ? 0 : t > C - 1 ? C - 1 : t;
+            float z = 0.f;
+            if (i < R) {
+                const float x = p.w[c * p.clip_stride + ((long)i * p.heads + a) * p.cols_full + t];
+                const float sv = sd[t];
+                if (sv > 0.f) z = p.half ? rh(rh(x - mu[t]) / sv) : (x - mu[t]) / sv;
             }
-            acc += win[pad];
+            zt[il][cl] = z;
         }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < COST_RT / 4; k++) {
+            const float* zr = &zt[ib + 4 * k][jl];
+            if (C <= pad) {
+                acc[k] += zr[pad];  // fewer columns than the half width: no filter
+            } else if (W == 7) {
+                float win[7];
+#pragma unroll
+                for (int q = 0; q < 7; q++) win[q] = zr[q];
+                acc[k] += median7(win);
+            } else {
+                float win[MZ_TS_MAX_WIDTH];
+                for (int q = 0; q < width; q++) {
+                    const float v = zr[q];
+                    int r = q - 1;
+                    while (r >= 0 && win[r] > v) {
+                        win[r + 1] = win[r];
+                        r--;
+                    }
+                    win[r + 1] = v;
+                }
+                acc[k] += win[pad];
+            }
+        }
+        __syncthreads();  // zt is rewritten for the next head
     }
-    float s = acc / (float)p.heads;
-    if (p.half) s = rh(s);
-    // DTW cell (i + 1, j + 1) lies on anti-diagonal i + j + 2
-    p.cost[c * p.diag_stride + (long)(i + j + 2) * p.ldd + (i + 1)] = s;
+#pragma unroll
+    for (int k = 0; k < COST_RT / 4; k++) {
+        float v = acc[k] / (float)p.heads;
+        if (p.half) v = rh(v);
+        val[ib + 4 * k][jl] = v;
+    }
+    __syncthreads();
+    // DTW cell (i + 1, j + 1) lies on anti-diagonal i + j + 2: tile diagonal dl = il + jl holds rows il of one run
+    float* dst = p.cost + c * p.diag_stride + (long)(i0 + j0 + 2) * p.ldd + (i0 + 1);
+    const int il = tid & 31;
+    for (int dl = tid >> 5; dl < COST_RT + COST_CT - 1; dl += 8) {
+        const int cl = dl - il;
+        if (cl >= 0 && cl < COST_CT && i0 + il < R && j0 + cl < C) dst[(long)dl * p.ldd + il] = val[il][cl];
+    }
 }
 
 // One workgroup per clip. Row i of the table (0..R) is handled by threads i, i + blockDim, ... The costs are staged
@@ -372,7 +401,7 @@ hipError_t mz_ts_launch(hipStream_t s, const MzTs& p, int n) {
     const dim3 gs((p.cols_full + 255) / 256, p.heads, n);
     hipLaunchKernelGGL(ts_stats_kernel, gs, dim3(256), 0, s, p);
     if (p.rmax > 0) {
-        const dim3 gc((p.cols_full + 255) / 256, p.rmax, n);
+        const dim3 gc((p.cols_full + COST_CT - 1) / COST_CT, (p.rmax + COST_RT - 1) / COST_RT, n);
         if (p.width == 7)
             hipLaunchKernelGGL(ts_cost_kernel<7>, gc, dim3(256), 0, s, p);
         else
