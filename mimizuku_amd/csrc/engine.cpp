@@ -163,6 +163,9 @@ struct mz_engine {
     int pending_n = 0;
     double pending_enq = 0;
     hipEvent_t enc_done = nullptr;
+    // the decode loop's end test: the rows' done flags copied to pinned memory a few steps before they are read
+    int* done_pin = nullptr;
+    hipEvent_t done_ev = nullptr;
     // kernel timing (mz_engine_profile): events around each encoder launch and each decoder step
     bool prof_on = false;
     struct Rec {
@@ -399,7 +402,10 @@ extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, in
             (r = mz_hip(hipEventCreateWithFlags(&e->join[k], hipEventDisableTiming), "hipEventCreate")))
             return fail(r);
     }
-    if ((r = mz_hip(hipEventCreateWithFlags(&e->enc_done, hipEventDisableTiming), "hipEventCreate"))) return fail(r);
+    if ((r = mz_hip(hipEventCreateWithFlags(&e->enc_done, hipEventDisableTiming), "hipEventCreate")) ||
+        (r = mz_hip(hipEventCreateWithFlags(&e->done_ev, hipEventDisableTiming), "hipEventCreate")) ||
+        (r = mz_hip(hipHostMalloc((void**)&e->done_pin, B * 4, hipHostMallocDefault), "hipHostMalloc (done)")))
+        return fail(r);
     if ((r = e->alloc(&e->xkvbuf, xkv_elems(*d, bmax))) || (r = e->alloc(&e->tok, B * mt)) ||
         (r = e->alloc(&e->done, B)) || (r = e->alloc(&e->ctr, 4)) || (r = e->alloc(&e->x, B * D)) ||
         (r = e->alloc(&e->h, B * D)) || (r = e->alloc(&e->datt, B * D)) ||
@@ -957,6 +963,8 @@ extern "C" int mz_engine_free(mz_engine* e) {
     if (e->graph) mz_graph_free(e->graph);
     hipStreamSynchronize(e->c->stream);
     if (e->enc_done) hipEventDestroy(e->enc_done);
+    if (e->done_ev) hipEventDestroy(e->done_ev);
+    if (e->done_pin) hipHostFree(e->done_pin);
     for (auto& r : e->recs) {
         hipEventDestroy(r.a);
         hipEventDestroy(r.b);
@@ -1076,13 +1084,24 @@ static int collect_impl(mz_engine* e, const int32_t* frames, int n, const int32_
         if (!e->graph || e->graph_b != n || e->graph_np != np)
             if (int r = mz_engine_capture(e, n, np)) return r;
     }
-    std::vector<int32_t> dn(n);
+    // Every 8 steps the loop ends if every row is done. The flags it reads were copied (asynchronously, into pinned
+    // memory) DONE_LAG steps earlier, so the steps enqueued since keep the device busy while the host waits for
+    // the copy and tests it: the queue never drains. A batch that finishes runs at most 8 + DONE_LAG - 1 steps
+    // more than it needs (finished rows skip their attention and keep eos).
+    constexpr int DONE_LAG = 2;
+    bool copied = false;
     while (steps < limit) {
         if (int r = use_graph ? mz_engine_replay(e) : mz_engine_step(e, n, 0, np)) return r;
         steps++;
-        if (steps % 8 == 0 && steps >= np) {
-            if (int r = mz_download(e->c, dn.data(), (uint64_t)(uintptr_t)e->done, (size_t)n * 4)) return r;
-            if (std::all_of(dn.begin(), dn.end(), [](int v) { return v != 0; })) break;
+        if (steps + DONE_LAG >= np && (steps + DONE_LAG) % 8 == 0) {
+            TRY(hipMemcpyAsync(e->done_pin, e->done, (size_t)n * 4, hipMemcpyDeviceToHost, e->c->stream), "done flags");
+            TRY(hipEventRecord(e->done_ev, e->c->stream), "hipEventRecord");
+            copied = true;
+        }
+        if (copied && steps % 8 == 0) {
+            TRY(hipEventSynchronize(e->done_ev), "done flags wait");
+            copied = false;
+            if (std::all_of(e->done_pin, e->done_pin + n, [](int v) { return v != 0; })) break;
         }
     }
     if (int r = mz_sync(e->c)) return r;
