@@ -212,7 +212,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
                     for (int r = 0; r < 16; r++)
                         st[(j * 32 + lr) * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)] = (f16)(acc[i][j][r] + bv);
                 }
-                __builtin_amdgcn_s_waitcnt(0);
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slice is in LDS (stores in flight stay)
                 __builtin_amdgcn_wave_barrier();
 #pragma unroll
                 for (int c = lane; c < WN * 8; c += 64) {
@@ -225,7 +225,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
                         *(f16x4*)dst = *(const f16x4*)&st[nl * 32 + ml];
                     }
                 }
-                __builtin_amdgcn_s_waitcnt(0);
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
                 __builtin_amdgcn_wave_barrier();  // the slice is read before the next one overwrites it
             }
             return;
