@@ -11,9 +11,11 @@
 //   ts_cost_kernel   one workgroup per 32 x 64 tile of (row, column): median of the width-w reflect-padded window
 //                    of z-scores, summed over heads; the cells are stored in anti-diagonal-major order
 //                    [d = i + j][i], so that the DTW reads each diagonal with consecutive addresses
-//   ts_dtw_kernel    one workgroup per clip: the DTW table is filled one anti-diagonal per step (every cell of a
-//                    diagonal depends only on the two previous diagonals, kept in LDS), the move taken into each cell
-//                    goes to a trace in the same diagonal-major order, and one lane walks the path back.
+//   ts_dtw_wave_kernel  tables of at most 256 rows: one wave per clip, four rows per lane, the previous two
+//                    anti-diagonals in registers and the moves packed in LDS, where one lane walks the path back
+//   ts_dtw_kernel    larger tables: one workgroup per clip; the DTW table is filled one anti-diagonal per step (every
+//                    cell of a diagonal depends only on the two previous diagonals, kept in LDS), the move taken into
+//                    each cell goes to a trace in the same diagonal-major order, and one lane walks the path back.
 #include <math.h>
 
 #include <algorithm>
