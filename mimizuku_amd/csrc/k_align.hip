@@ -7,7 +7,8 @@
 // off, so both give identical bits.
 //
 // Three launches per batch of clips:
-//   ts_stats_kernel  one thread per (clip, head, column): mean and population standard deviation over the rows
+//   ts_stats_kernel  one thread per (clip, head, column) (ts_stats4_kernel: four adjacent columns per thread): mean
+//                    and population standard deviation over the rows
 //   ts_cost_kernel   one workgroup per 32 x 64 tile of (row, column): median of the width-w reflect-padded window
 //                    of z-scores, summed over heads; the cells are stored in anti-diagonal-major order
 //                    [d = i + j][i], so that the DTW reads each diagonal with consecutive addresses
@@ -82,6 +83,75 @@ __global__ void __launch_bounds__(256) ts_stats_kernel(const MzTs p) {
     const long o = ((long)c * p.heads + a) * p.cols_full + j;
     p.mean[o] = mu;
     p.sd[o] = sd;
+}
+
+// The same statistics for four adjacent columns per thread through 16-byte loads (each column's sums in row order,
+// exactly as above): for rows whose column count and clip stride are multiples of 4 at a 16-byte aligned base
+// (every engine batch: 1500 columns). Columns past C are summed (their reads stay inside the row) but not stored.
+__global__ void __launch_bounds__(256) ts_stats4_kernel(const MzTs p) {
+    const int c = blockIdx.z, a = blockIdx.y, j = (blockIdx.x * 256 + threadIdx.x) * 4;
+    const int R = p.rc[c].x, C = p.rc[c].y;
+    if (j >= C || R <= 0) return;
+    const float4* w = (const float4*)(p.w + c * p.clip_stride + (long)a * p.cols_full + j);
+    const long rs = (long)p.heads * p.cols_full / 4;
+    float mu[4], sd[4];
+    if (p.half) {
+        float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll 4
+        for (int i = 0; i < R; i++) {
+            const float4 v = w[i * rs];
+            s0 += v.x;
+            s1 += v.y;
+            s2 += v.z;
+            s3 += v.w;
+        }
+        const float m0 = s0 / (float)R, m1 = s1 / (float)R, m2 = s2 / (float)R, m3 = s3 / (float)R;
+        float q0 = 0.f, q1 = 0.f, q2 = 0.f, q3 = 0.f;
+#pragma unroll 4
+        for (int i = 0; i < R; i++) {
+            const float4 v = w[i * rs];
+            const float d0 = v.x - m0, d1 = v.y - m1, d2 = v.z - m2, d3 = v.w - m3;
+            q0 += d0 * d0;
+            q1 += d1 * d1;
+            q2 += d2 * d2;
+            q3 += d3 * d3;
+        }
+        mu[0] = rh(m0), mu[1] = rh(m1), mu[2] = rh(m2), mu[3] = rh(m3);
+        sd[0] = rh(__builtin_sqrtf(q0 / (float)R)), sd[1] = rh(__builtin_sqrtf(q1 / (float)R));
+        sd[2] = rh(__builtin_sqrtf(q2 / (float)R)), sd[3] = rh(__builtin_sqrtf(q3 / (float)R));
+    } else {
+        double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+#pragma unroll 4
+        for (int i = 0; i < R; i++) {
+            const float4 v = w[i * rs];
+            s0 += (double)v.x;
+            s1 += (double)v.y;
+            s2 += (double)v.z;
+            s3 += (double)v.w;
+        }
+        const float m0 = (float)(s0 / R), m1 = (float)(s1 / R), m2 = (float)(s2 / R), m3 = (float)(s3 / R);
+        double q0 = 0.0, q1 = 0.0, q2 = 0.0, q3 = 0.0;
+#pragma unroll 4
+        for (int i = 0; i < R; i++) {
+            const float4 v = w[i * rs];
+            const double d0 = (double)(v.x - m0), d1 = (double)(v.y - m1), d2 = (double)(v.z - m2),
+                         d3 = (double)(v.w - m3);
+            q0 += d0 * d0;
+            q1 += d1 * d1;
+            q2 += d2 * d2;
+            q3 += d3 * d3;
+        }
+        mu[0] = m0, mu[1] = m1, mu[2] = m2, mu[3] = m3;
+        sd[0] = __builtin_sqrtf((float)(q0 / R)), sd[1] = __builtin_sqrtf((float)(q1 / R));
+        sd[2] = __builtin_sqrtf((float)(q2 / R)), sd[3] = __builtin_sqrtf((float)(q3 / R));
+    }
+    const long o = ((long)c * p.heads + a) * p.cols_full + j;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        if (j + e < C) {
+            p.mean[o + e] = mu[e];
+            p.sd[o + e] = sd[e];
+        }
 }
 
 // One workgroup per tile of COST_RT rows x COST_CT columns of a clip. Per head, the tile's z-scores (with the window's
@@ -400,8 +470,13 @@ hipError_t mz_ts_launch(hipStream_t s, const MzTs& p, int n) {
     if (p.width < 1 || p.width % 2 == 0 || p.width > MZ_TS_MAX_WIDTH || p.heads <= 0 || p.rmax < 0 ||
         p.ldd < p.rmax + 1 || p.cols_full <= 0)
         return hipErrorInvalidValue;
-    const dim3 gs((p.cols_full + 255) / 256, p.heads, n);
-    hipLaunchKernelGGL(ts_stats_kernel, gs, dim3(256), 0, s, p);
+    if (p.cols_full % 4 == 0 && p.clip_stride % 4 == 0 && ((uintptr_t)p.w & 15) == 0) {
+        const dim3 gs((p.cols_full / 4 + 255) / 256, p.heads, n);
+        hipLaunchKernelGGL(ts_stats4_kernel, gs, dim3(256), 0, s, p);
+    } else {
+        const dim3 gs((p.cols_full + 255) / 256, p.heads, n);
+        hipLaunchKernelGGL(ts_stats_kernel, gs, dim3(256), 0, s, p);
+    }
     if (p.rmax > 0) {
         const dim3 gc((p.cols_full + COST_CT - 1) / COST_CT, (p.rmax + COST_RT - 1) / COST_RT, n);
         if (p.width == 7)

@@ -412,6 +412,22 @@ def test_timestamps_device_row_limits(ctx, rows, cols):
                                       err_msg=f"clip {c}")
 
 
+@pytest.mark.parametrize("full", [1500, 203])
+def test_timestamps_device_column_layouts(ctx, full):
+    """Rows of 1500 columns (four columns per thread in the column statistics) and of an odd count (one per thread):
+    identical floats in both modes."""
+    from mimizuku_amd import transcribe
+    rng = np.random.default_rng(full)
+    heads, rows, cols = 3, [12, 30, 7], [full, full - 1, full // 2]
+    w = softmax_rows(rng, (3, 30, heads, full))
+    dw = ctx.upload_new(w)
+    for half in (False, True):
+        got = transcribe.jump_times_device(ctx, dw, 30 * heads * full, rows, cols, heads, full, 7, half)
+        for c in range(3):
+            np.testing.assert_array_equal(got[c], transcribe.jump_times(w[c, :rows[c]], cols[c], 7, half),
+                                          err_msg=f"clip {c} half {half}")
+
+
 def test_timestamps_device_other_widths(ctx):
     from mimizuku_amd import transcribe
     rng = np.random.default_rng(5)
