@@ -19,7 +19,9 @@ error of its score, ~1e-3 here from the fp16 rounding of the LayerNorm output th
 it in fp32; the reference rounds it, as this build does).
 
 At the benchmark's own positions (200 .. 203, the self-attention cache holding 200+ keys) every decoder layer is
-checked layer-local on the engine's residual trace, and the logits of its final residual against the oracle's head.
+checked layer-local on the engine's residual trace, and the logits of its final residual against the oracle's head;
+and the step as the benchmark runs it, one captured graph replayed through positions 0 .. 205 of a 200-token prompt,
+gives the same bits as eager steps.
 """
 import numpy as np
 import pytest
@@ -183,5 +185,51 @@ def test_decoder_turbo_widths_at_position_200():
         worst_lg = max(worst_lg, rel_err(e.logits()[:B], ref))
     print("turbo widths, B = 32, positions 200..203: layer-local max-abs / RMS", worst, "; logits", worst_lg)
     assert worst_lg <= 2e-3
+    e.close()
+    ctx.close()
+
+
+def test_graph_replay_at_position_200_equals_eager():
+    """The benchmark's replayed step against eager steps at its own shape: 32 rows, a 200-token prompt, 206 steps
+    (positions 0 .. 205, greedy choices from position 200 on). One captured graph replayed 206 times gives the same
+    bits as 206 eager launches of the same kernels: every token, the final residual and logits of the last step, the
+    alignment rows of positions 196 .. 205 and both self-attention caches."""
+    rng = np.random.default_rng(23)
+    W = synth.random_weights(G, seed=7, bias_std=0.02, ln_std=0.1)
+    gen = synth.generation_config(G, align_heads=[[2, 4], [2, 11], [3, 3], [3, 6], [3, 11], [3, 14]])
+    dims = model.Dims(G.d, G.ff, G.nh, G.enc_layers, G.dec_layers, G.n_mels, G.vocab, G.max_t)
+    gc = model.GenCfg.from_dict(gen, dims)
+    xkv = np.zeros((B, G.dec_layers, 2, G.nh, TPAD, 64), np.float16)
+    for b in range(B):
+        xkv[b, :, :, :, :1500] = rng.standard_normal((G.dec_layers, 2, G.nh, 1500, 64), dtype=np.float32)
+    npr, steps = 200, 206
+    prompts = rng.integers(0, 50000, size=(B, npr)).astype(np.int32)
+    ctx = model.Context(0)
+    e = model.Engine(ctx, dims, gc, B, 8)
+    e.load(W)
+    p, _ = e.buffer(L.BUF_XKV)
+    ctx.upload(p, xkv)
+    del xkv
+
+    def state():
+        kc, vc = e.self_kv()
+        return (e.tokens()[:B, :steps + 1], e.dec_x()[:B], e.logits()[:B], e.align()[:B, steps - 10:steps],
+                kc[:, :B, :, :steps], vc[:, :B, :, :steps])
+
+    e.reset(prompts)
+    for _ in range(steps):
+        e.step(B, False, npr)
+    eager = state()
+    e.reset(prompts)
+    e.capture(B, npr)
+    for _ in range(steps):
+        e.replay()
+    graph = state()
+    names = ("tokens", "final residual", "logits", "alignment rows", "self keys", "self values")
+    for n, a, g in zip(names, eager, graph):
+        np.testing.assert_array_equal(a, g, err_msg=n)
+    assert np.all(eager[0][:, :npr] == prompts)
+    print("turbo widths, B = 32: graph replay = eager steps over positions 0 ..", steps - 1, "; generated",
+          eager[0][:4, npr:].tolist(), "...")
     e.close()
     ctx.close()
