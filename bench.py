@@ -305,6 +305,24 @@ def run_model(g, seed: int, steps: int, warmup: int, graph: bool, label: str, L,
     ctx.sync()
     r["dec_prof"] = {k: v for k, v in e.profile_read().items() if k.startswith("dec_")}
     e.profile(False)
+    # the same step at 8 rows and at 1 (a single clip, the last partial chunk of a batch), graph replay only
+    r["step_small"] = {}
+    for bs in ((8, 1) if graph else ()):
+        e.reset(pr[:bs])
+        e.capture(bs, nprompt)
+        for _ in range(200):
+            e.replay()
+        ctx.sync()
+        e.profile(True)
+        for _ in range(20):
+            e.replay()
+        st_ms, st_n = e.profile_read()["step"]
+        e.profile(False)
+        us = st_ms / st_n * 1e3
+        nb = float(np.mean([decode_step_bytes(g, bs, p, r["na"]) for p in range(200, 220)]))
+        r["step_small"][bs] = {"us": round(us, 2), "mb": round(nb / 1e6, 1),
+                               "hbm_frac": round(nb / (us * 1e-6) / PEAK_HBM, 4)}
+        log(f"bench: {label} decode step at B={bs}, p=200..219: {us:.1f} us, {nb / (us * 1e-6) / 1e9:.0f} GB/s")
     return ctx, e, dmel, r
 
 
@@ -441,6 +459,10 @@ def main():
         "decode_step_us": round(r["step_us"], 2),
         "decode_step_hbm_frac": round(r["step_bytes"] / (r["step_us"] * 1e-6) / PEAK_HBM, 4),
         "decode_step_us_e2e_avg": round(r["dec_s"] / r["nsteps"] * 1e6, 2),
+        "decode_step_small_batch": {f"b{bs}": v for bs, v in r["step_small"].items()},
+        "decode_step_small_batch_note": "graph replay at p = 200..219 with 8 rows and with 1 row; mb = the "
+                                        "algorithmic HBM bytes of one step (weights, LM head, cross and self keys / "
+                                        "values of those rows), hbm_frac against 8 TB/s",
         "host_mel_audio_s_per_s": round(r["host_mel_value"], 2),
         "host_mel_note": "the same step with the log-mel in host memory (pinned staging, asynchronous copies per "
                          "encoder lane), 2 steps: the PCIe-inclusive rate, not the headline value",

@@ -241,7 +241,10 @@ typedef struct {
  * prompt = [sot, lang, task, notimestamps] (lang ignored when detect != 0). max_new caps the generated tokens
  * (<= 0: up to max_t - prompt_len, as the reference). half_align != 0 rounds the timestamp arithmetic through fp16
  * as the reference does (src/align.rs). Outputs per clip i: seq[i * max_t ..] tokens, seq_len[i], ts[i * max_t ..]
- * start times, langs[i]. */
+ * start times, langs[i]. The decoding loop tests the done flags every 8 steps, as the reference's (transcribe.rs:
+ * 136-141), but reads flags copied two steps earlier so that the device never waits for the host: a batch whose last
+ * row finishes in the last two steps before a multiple of 8 runs 8 steps more than the reference's loop, and
+ * times->steps is then 8 larger. Tokens, lengths and times are the same (finished rows keep eos). */
 int mz_transcribe(mz_engine* e, const float* mels, const int32_t* frames, int n, const int32_t* prompt,
                   int prompt_len, int detect, int use_graph, int max_new, int half_align, int32_t* seq,
                   int32_t* seq_len, float* ts, int32_t* langs, mz_times* times);
@@ -274,8 +277,9 @@ int mz_jump_times_device(mz_ctx* c, uint64_t w, int64_t clip_stride, int n, cons
  * arguments and results as mz_jump_times_device (bit for bit). Its scratch is a static 64 MiB array per device
  * (held until the process ends), located by mz_init; the clips go through it in passes of at most 64 that fit, and a
  * clip whose own scratch exceeds 64 MiB is refused with MZ_ERR_ARG (e.g. more than about 1,200 rows at 1500 frames).
- * Every call on a device shares that device's array: calls that overlap on one GPU (other threads, other contexts)
- * race and must be serialised by the caller. Synchronous on the context's stream. */
+ * Every call on a device shares that device's array (one copy per process and GPU), so the library serialises them:
+ * a call holds a per-device lock from its first use of the array until its results are on the host, and calls from
+ * other threads or contexts on the same GPU wait for it. Synchronous on the context's stream. */
 int mz_jump_times_device_noalloc(mz_ctx* c, uint64_t w, int64_t clip_stride, int n, const int32_t* rows,
                                  const int32_t* cols, int heads, int cols_full, int width, int half, float* out,
                                  int64_t out_stride);

@@ -238,6 +238,14 @@ int ksplit_for(int N, int K) {
     return best;
 }
 
+// elements of the decoder's split-K partials buffer: the largest ks * rows * n over the decoder products
+size_t part_elems(int D, int F, int B) {
+    size_t pe = 0;
+    for (auto nk : {std::pair<int, int>{D, D}, {D, F}, {3 * D, D}})
+        pe = std::max(pe, (size_t)ksplit_for(nk.first, nk.second) * B * nk.first);
+    return pe;
+}
+
 }  // namespace
 
 extern "C" size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int eg) {
@@ -249,7 +257,7 @@ extern "C" size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int 
     size_t dec = B * nl * 2 * nh * TPAD * HD * 2 + B * mt * 4 + B * 4 + 16 + B * D * 4 + B * D * 2 * 2 + B * F * 2 +
                  2 * nl * B * nh * mt * HD * 2 + B * V * 4 + B * mt * n_align * TENC * 4 + (size_t)mz_lm_blocks((int)V) * B * 8 +
                  nl * nh * 4 + 2 * V;
-    size_t part = (size_t)MZ_MAX_PARTS * B * D * 4;
+    size_t part = part_elems((int)D, (int)F, (int)B) * 4;
     size_t ts = B * 8 + 2 * B * n_align * TENC * 4 + B * (size_t)mz_ts_diag_stride((int)mt - 1, TENC) * 5 + B * mt * 4;
     return MZ_ENC_LANES * enc + dec + part + ts;
 }
@@ -420,10 +428,7 @@ extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, in
         (r = e->alloc(&e->ts_sd, B * e->na * (size_t)TENC)) || (r = e->alloc(&e->ts_cost, B * tsd)) ||
         (r = e->alloc(&e->ts_trace, B * tsd)) || (r = e->alloc(&e->ts_out, B * mt)))
         return fail(r);
-    // split-K partials: the largest ks * rows * n over the decoder products
-    size_t pe = 0;
-    for (auto nk : {std::pair<int, int>{D, D}, {D, F}, {3 * D, D}})
-        pe = std::max(pe, (size_t)ksplit_for(nk.first, nk.second) * B * nk.first);
+    const size_t pe = part_elems(D, F, (int)B);
     e->part_elems = pe;
     if ((r = e->alloc(&e->part, pe))) return fail(r);
 

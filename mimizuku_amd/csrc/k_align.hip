@@ -411,7 +411,10 @@ __global__ void __launch_bounds__(64) ts_dtw_wave_kernel(const MzTs p) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const float c0 = r ? D2[r - 1] : up2, c1 = r ? D1[r - 1] : up1, c2 = D1[r];
-                const bool t0 = c0 < fminf(c1, c2), t1 = c1 < fminf(c0, c2);  // no NaN among inside cells
+                // the reference's comparisons as written (align.rs:77-83), so a NaN cost (a NaN or infinite
+                // z-score in half mode) picks the same move as the host routine and ts_dtw_kernel: fminf would
+                // drop the NaN operand
+                const bool t0 = (c0 < c1) & (c0 < c2), t1 = (c1 < c0) & (c1 < c2);
                 const float m = t0 ? c0 : t1 ? c1 : c2;
                 // ts_dtw_kernel's fp64 -x + m rounded to fp32 equals the fp32 m - x: a sum rounded first to 53 bits
                 // and then to 24 rounds as if once, since 53 >= 2 x 24 + 2 (Figueroa, 1995)
@@ -508,6 +511,8 @@ namespace {
 constexpr int MZ_MAX_DEVICES = 64;
 std::mutex g_scratch_mu;
 void* g_scratch[MZ_MAX_DEVICES] = {};
+// held by a call of mz_jump_times_device_noalloc for its whole use of that device's array
+std::mutex g_scratch_use[MZ_MAX_DEVICES];
 size_t up256(size_t n) { return (n + 255) & ~(size_t)255; }
 }  // namespace
 
@@ -544,6 +549,9 @@ extern "C" int mz_jump_times_device_noalloc(mz_ctx* c, uint64_t w, int64_t clip_
         std::lock_guard<std::mutex> lock(g_scratch_mu);
         base = (unsigned char*)g_scratch[c->device];
     }
+    // the array is this device's only copy: calls from other threads (or contexts) on the same GPU wait until this
+    // one's results are on the host (every chunk below ends with a synchronisation of the stream)
+    std::lock_guard<std::mutex> use(g_scratch_use[c->device]);
     // scratch of k clips whose longest has rmax rows: (rows, columns), column statistics, DTW cost and trace, times
     auto need = [&](int k, int rmax) {
         return up256((size_t)k * sizeof(int2)) + 2 * up256((size_t)k * heads * cols_full * 4) +

@@ -49,9 +49,10 @@ def gelu(x: np.ndarray) -> np.ndarray:
 
 def linear(x: np.ndarray, w: np.ndarray, b: np.ndarray | None = None) -> np.ndarray:
     """y = x Wᵀ + b in fp32 (nn.Linear)."""
-    y = x.astype(np.float32) @ w.astype(np.float32).T
+    # (np.asarray: no copy of a weight that is already float32)
+    y = np.asarray(x, np.float32) @ np.asarray(w, np.float32).T
     if b is not None:
-        y = y + b.astype(np.float32)
+        y = y + np.asarray(b, np.float32)
     return y
 
 
@@ -163,9 +164,9 @@ class Decoder:
 
     def step(self, toks: list[int], p: int):
         W, nh = self.W, self.nh
-        emb = W["model.decoder.embed_tokens.weight"].astype(np.float32)
-        pe = W["model.decoder.embed_positions.weight"].astype(np.float32)
-        x = np.stack([emb[t] + pe[p] for t in toks])  # [B, d]
+        emb = W["model.decoder.embed_tokens.weight"]
+        pe = W["model.decoder.embed_positions.weight"]
+        x = np.stack([emb[t].astype(np.float32) + pe[p].astype(np.float32) for t in toks])  # [B, d]
         probs = np.zeros((len(toks), self.nl, nh, TENC), np.float32)
         for i in range(self.nl):
             cache = [(_heads(np.stack(self.kc[b][i]), nh) if self.kc[b][i] else None,

@@ -12,10 +12,11 @@ that hold at any size, and the oracle checks a subsample of it layer-local:
 * alignment rows of every fed position: finite, non-negative, each summing to 1;
 * timestamps: zero over the prompt, non-decreasing, within the clip, the last token repeating the one before, and
   bit-equal to the host routine (mz_jump_times) on the downloaded alignment rows;
-* the oracle: the conv stem and encoder layers 0, 16 and 31 of one clip layer-local; decoder layers 0, 15 and 31 and
-  the LM head of two rows layer-local at two teacher-forced positions of their own transcription (max-abs error
-  <= 2e-3 x RMS), and the transcription's token equal to the oracle's choice on those logits wherever the oracle's
-  top-2 margin exceeds 1e-2.
+* the oracle: the conv stem and encoder layers 0, 16 and 31 of one clip layer-local; decoder layers 0, 15 and 31 of
+  two rows layer-local at two teacher-forced positions of their own transcription (max-abs error <= 2e-3 x RMS); and
+  for every row at every teacher-forced generated position (12 per row), the LM head layer-local (the final LayerNorm
+  and the tied head on the engine's own final residual, <= 2e-3 x RMS) and the transcription's token equal to the
+  oracle's choice on those logits wherever the oracle's top-2 margin exceeds 1e-2.
 """
 import inspect
 
@@ -142,8 +143,9 @@ def test_oracle_subsample_layer_local(run):
     assert max(errs) <= 2e-3, errs
     del We
 
-    # decoder: rows 3 and 20 teacher-forced on their own transcriptions (all 32 rows stepped eagerly)
-    rows, T, dec_layers = [3, 20], 10, (0, 15, 31)
+    # decoder: every row teacher-forced on its own transcription (all 32 rows stepped eagerly); rows 3 and 20
+    # through decoder layers 0, 15 and 31 at the last two positions
+    rows, T, dec_layers = [3, 20], NP + 12, (0, 15, 31)
     Wd = f32([k for k in W if k.startswith("model.decoder.") and
               (not k.startswith("model.decoder.layers.") or int(k.split(".")[3]) in dec_layers)])
     seqs = np.array([(s.seq + [gen["eos_token_id"]] * T)[:T] for s in out], np.int32)
@@ -152,11 +154,28 @@ def test_oracle_subsample_layer_local(run):
     cross = {(l, r): e.read(L.BUF_XKV, np.float16, (2, nh, TPAD, 64), ((r * nl + l) * tile) * 2)
              for l in dec_layers for r in rows}
     kv_plane = nh * G.max_t * 64
-    sup = set(gen["suppress_tokens"])
+    sup, bsup = set(gen["suppress_tokens"]), gen["begin_suppress_tokens"]
+    emb = Wd["model.decoder.embed_tokens.weight"]
     worst = worst_lg = 0.0
-    checked = 0
+    checked, rows_checked = 0, set()
     for p in range(T - 1):
         e.step(B, False, T)
+        if p < NP - 1:
+            continue
+        # every row: the LM head layer-local, and the transcription's token against the oracle's choice
+        xf = e.dec_x()[:B]
+        h = R.layer_norm(xf, Wd["model.decoder.layer_norm.weight"], Wd["model.decoder.layer_norm.bias"])
+        ref_all = R.linear(h, emb)
+        lg_all = e.logits()[:B]
+        err = rel_err(lg_all, ref_all)
+        worst_lg = max(worst_lg, err)
+        assert err <= 2e-3, (p, "logits", err)
+        first = p + 1 == NP
+        for r in range(B):
+            if len(out[r].seq) > p + 1 and R.top2_margin(ref_all[r], sup, bsup, first) > 1e-2:
+                assert out[r].seq[p + 1] == R.choose(ref_all[r], sup, bsup, first, gen["eos_token_id"], False), (p, r)
+                checked += 1
+                rows_checked.add(r)
         if p < T - 3:
             continue
         tr = e.dec_trace()[:, rows]
@@ -172,17 +191,7 @@ def test_oracle_subsample_layer_local(run):
             err = rel_err(tr[l + 1], ref)
             worst = max(worst, err)
             assert err <= 2e-3, (p, l, err)
-        h = R.layer_norm(tr[nl], Wd["model.decoder.layer_norm.weight"], Wd["model.decoder.layer_norm.bias"])
-        ref = R.linear(h, Wd["model.decoder.embed_tokens.weight"])
-        lg = e.logits()[rows]
-        err = rel_err(lg, ref)
-        worst_lg = max(worst_lg, err)
-        assert err <= 2e-3, (p, "logits", err)
-        for i, r in enumerate(rows):
-            if len(out[r].seq) > p + 1 and R.top2_margin(ref[i], sup, [], False) > 1e-2:
-                assert out[r].seq[p + 1] == R.choose(ref[i], sup, [], False, gen["eos_token_id"], False), (p, r)
-                checked += 1
     e.set_trace(False)
-    print("large-v3 e2e, rows 3 and 20: decoder layers 0 / 15 / 31 max-abs / RMS", worst, "; LM head", worst_lg,
-          "; choices checked", checked)
-    assert checked >= 2
+    print("large-v3 e2e, rows 3 and 20: decoder layers 0 / 15 / 31 max-abs / RMS", worst, "; LM head (32 rows,",
+          T - NP, "positions)", worst_lg, "; choices checked", checked, "in", len(rows_checked), "rows")
+    assert len(rows_checked) >= 8 and checked >= 8 * 8

@@ -412,6 +412,29 @@ def test_timestamps_device_row_limits(ctx, rows, cols):
                                       err_msg=f"clip {c}")
 
 
+def test_timestamps_device_nan_costs(ctx):
+    """A column whose values overflow fp16 (0 and 2e5 alternating: mean and deviation round to inf, z = inf / inf)
+    gives NaN DTW costs in half mode. The DTW must then choose its moves with the reference's comparisons as written
+    (a NaN neighbour loses every comparison, align.rs:77-83), in the one-wave kernel (<= 255 rows) as in the
+    workgroup kernel and the host routine: identical floats."""
+    from mimizuku_amd import transcribe
+    rng = np.random.default_rng(29)
+    heads, full = 6, 1500
+    rows, cols = [40, 255, 7, 300], [1500, 1500, 900, 1500]
+    rmax = max(rows)
+    w = softmax_rows(rng, (len(rows), rmax, heads, full))
+    for c, col in enumerate((700, 1201, 450, 333)):
+        w[c, 0::2, :, col] = 0.0
+        w[c, 1::2, :, col] = 2e5
+    for c in range(len(rows)):
+        assert np.isnan(transcribe.align_cost(w[c, :rows[c]], cols[c], 7, True)).any(), f"clip {c}: no NaN cost"
+    dw = ctx.upload_new(w)
+    got = transcribe.jump_times_device(ctx, dw, rmax * heads * full, rows, cols, heads, full, 7, True)
+    for c in range(len(rows)):
+        np.testing.assert_array_equal(got[c], transcribe.jump_times(w[c, :rows[c]], cols[c], 7, True),
+                                      err_msg=f"clip {c} ({rows[c]} rows)")
+
+
 @pytest.mark.parametrize("full", [1500, 203])
 def test_timestamps_device_column_layouts(ctx, full):
     """Rows of 1500 columns (four columns per thread in the column statistics) and of an odd count (one per thread):

@@ -141,12 +141,15 @@ def test_decoder_turbo_widths_batch32():
     ctx.close()
 
 
-def test_decoder_turbo_widths_at_position_200():
+@pytest.mark.parametrize("nb", [32, 8, 1])
+def test_decoder_turbo_widths_at_position_200(nb):
     """The benchmark's decoder step shape: 32 rows at positions 200 .. 203, the self-attention cache holding 200+
-    keys. Every decoder layer layer-local (the oracle's layer on the engine's own residual, cache and cross
-    keys / values) within 2e-3 x RMS, and the logits of the engine's final residual (the final LayerNorm and the tied
-    LM head, layer-local) within 2e-3 x RMS."""
-    rng = np.random.default_rng(22)
+    keys; and the same with 8 rows and with 1 (a single clip, or the last partial chunk of a batch: the skinny
+    products then run with most of their 32-row MFMA operand zero). Every decoder layer layer-local (the oracle's layer
+    on the engine's own residual, cache and cross keys / values) within 2e-3 x RMS, and the logits of the engine's
+    final residual (the final LayerNorm and the tied LM head, layer-local) within 2e-3 x RMS."""
+    B = nb
+    rng = np.random.default_rng(22 + nb)
     W = synth.random_weights(G, seed=6, bias_std=0.02, ln_std=0.1)
     Wf = {k: v.astype(np.float32) for k, v in W.items() if k.startswith("model.decoder")}
     gen = synth.generation_config(G, align_heads=[[2, 4], [2, 11], [3, 3], [3, 6], [3, 11], [3, 14]])
@@ -158,7 +161,7 @@ def test_decoder_turbo_widths_at_position_200():
     npr = 204
     prompts = rng.integers(0, 50000, size=(B, npr)).astype(np.int32)
     ctx = model.Context(0)
-    e = model.Engine(ctx, dims, gc, B, 8)
+    e = model.Engine(ctx, dims, gc, B, min(8, B))
     e.load(W)
     e.set_trace(True)
     p, _ = e.buffer(L.BUF_XKV)
@@ -183,7 +186,7 @@ def test_decoder_turbo_widths_at_position_200():
         h = R.layer_norm(tr[-1], Wf["model.decoder.layer_norm.weight"], Wf["model.decoder.layer_norm.bias"])
         ref = R.linear(h, Wf["model.decoder.embed_tokens.weight"])
         worst_lg = max(worst_lg, rel_err(e.logits()[:B], ref))
-    print("turbo widths, B = 32, positions 200..203: layer-local max-abs / RMS", worst, "; logits", worst_lg)
+    print(f"turbo widths, B = {B}, positions 200..203: layer-local max-abs / RMS", worst, "; logits", worst_lg)
     assert worst_lg <= 2e-3
     e.close()
     ctx.close()

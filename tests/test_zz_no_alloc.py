@@ -56,3 +56,45 @@ def test_noalloc_refuses_a_clip_beyond_its_scratch(ctx):
     with pytest.raises(L.MzError, match="static scratch"):
         transcribe.jump_times_device_noalloc(ctx, dw, heads * full, [1], [full], heads, full, 7, True)
     ctx.free(dw)
+
+
+def test_noalloc_two_threads_on_one_context(ctx):
+    """Two host threads calling the entry point on one context share the device's one static array: the library
+    holds a per-device lock for each whole call, so every result equals the allocating entry point's."""
+    import threading
+    rng = np.random.default_rng(41)
+    heads, full = 6, 1500
+    jobs = []
+    for t in range(2):
+        n, rmax = (24, 200) if t == 0 else (9, 90)
+        rows = rng.integers(1, rmax + 1, size=n).astype(np.int32)
+        cols = rng.integers(1, full + 1, size=n).astype(np.int32)
+        w = softmax_rows(rng, (n, rmax, heads, full))
+        dw = ctx.upload_new(w)
+        stride = rmax * heads * full
+        ref = transcribe.jump_times_device(ctx, dw, stride, rows, cols, heads, full, 7, True)
+        jobs.append((dw, stride, rows, cols, ref))
+    results = [[None] * 4 for _ in range(2)]
+    errors = []
+
+    def run(t):
+        dw, stride, rows, cols, _ = jobs[t]
+        try:
+            for k in range(4):
+                results[t][k] = transcribe.jump_times_device_noalloc(ctx, dw, stride, rows, cols, heads, full, 7, True)
+        except Exception as ex:  # reported below, in the main thread
+            errors.append(ex)
+
+    threads = [threading.Thread(target=run, args=(t,)) for t in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=100)
+    assert not any(th.is_alive() for th in threads), "a thread did not finish"
+    assert not errors, errors
+    for t in range(2):
+        ref = jobs[t][4]
+        for k in range(4):
+            for c in range(len(ref)):
+                np.testing.assert_array_equal(results[t][k][c], ref[c], err_msg=f"thread {t} call {k} clip {c}")
+        ctx.free(jobs[t][0])
