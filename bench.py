@@ -65,7 +65,9 @@ def dec_kernel_bytes(g, B: int, p: int, na: int) -> dict:
         "dec_self": B * 2 * (p + 1) * d * 2 + B * d * 4 + act,
         "dec_oproj": d * d * 2 + act + ks_dd * B * d * 4,
         "dec_addln": B * d * 4 * (ks_dd + 2) + act,
-        "dec_cross": B * 2 * 1500 * d * 2 + d * d * 2 + 2 * act + B * (na / nl) * 1500 * 4,
+        # keys and values, the query weights, the residual add of the out-projection's partials (read x and the
+        # partials, write the new residual) and the output, the alignment rows
+        "dec_cross": B * 2 * 1500 * d * 2 + d * d * 2 + B * d * 4 * (ks_dd + 2) + act + B * (na / nl) * 1500 * 4,
         "dec_xo": d * d * 2 + act + ks_dd * B * d * 4,
         "dec_fc1": ff * d * 2 + act + B * ff * 2,
         "dec_fc2": d * ff * 2 + B * ff * 2 + ks_df * B * d * 4,
@@ -320,8 +322,15 @@ def run_model(g, seed: int, steps: int, warmup: int, graph: bool, label: str, L,
         e.profile(False)
         us = st_ms / st_n * 1e3
         nb = float(np.mean([decode_step_bytes(g, bs, p, r["na"]) for p in range(200, 220)]))
+        # per kernel class: HIP events around each launch of three eager steps (p = 220..222)
+        e.profile(True)
+        for _ in range(3):
+            e.step(bs, False, nprompt)
+        ctx.sync()
+        kp = {k: round(ms / n * 1e3, 2) for k, (ms, n) in e.profile_read().items() if k.startswith("dec_") and n}
+        e.profile(False)
         r["step_small"][bs] = {"us": round(us, 2), "mb": round(nb / 1e6, 1),
-                               "hbm_frac": round(nb / (us * 1e-6) / PEAK_HBM, 4)}
+                               "hbm_frac": round(nb / (us * 1e-6) / PEAK_HBM, 4), "kernel_avg_us": kp}
         log(f"bench: {label} decode step at B={bs}, p=200..219: {us:.1f} us, {nb / (us * 1e-6) / 1e9:.0f} GB/s")
     return ctx, e, dmel, r
 
@@ -462,7 +471,8 @@ def main():
         "decode_step_small_batch": {f"b{bs}": v for bs, v in r["step_small"].items()},
         "decode_step_small_batch_note": "graph replay at p = 200..219 with 8 rows and with 1 row; mb = the "
                                         "algorithmic HBM bytes of one step (weights, LM head, cross and self keys / "
-                                        "values of those rows), hbm_frac against 8 TB/s",
+                                        "values of those rows), hbm_frac against 8 TB/s; kernel_avg_us: HIP events "
+                                        "around each launch of three eager steps",
         "host_mel_audio_s_per_s": round(r["host_mel_value"], 2),
         "host_mel_note": "the same step with the log-mel in host memory (pinned staging, asynchronous copies per "
                          "encoder lane), 2 steps: the PCIe-inclusive rate, not the headline value",

@@ -800,10 +800,6 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
         a.na = e->na;
         return a;
     };
-    auto attn = [&](const float* q, int nq, const f16* wq, const f16* qbias, const f16* k, const f16* v, long kv_b,
-                    int L, const int* aslot) {
-        return mz_dec_attn_launch(s, attn_args(q, nq, wq, qbias, k, v, kv_b, L, aslot));
-    };
     const int ks_dd = ksplit_for(D, D), ks_df = ksplit_for(D, F), ks_qkv = ksplit_for(3 * D, D);
     const f16* xkv = e->xkvbuf;
     for (int i = 0; i < nl; i++) {
@@ -824,22 +820,41 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
         }
         PROF(MZ_K_DEC_OPROJ, gemm(DEPI_PARTIAL, e->datt, D, L.o, D, D, ks_dd, e->part, D), "dec out-proj");
         PROF(MZ_K_DEC_ADDLN,
-             mz_dec_add_ln_launch(s, e->x, e->part, ks_dd, (long)b * D, L.o.b, L.lnx.w, L.lnx.b, e->h, b, D, EPS),
+             mz_dec_add_ln_launch(s, e->x, e->x, e->part, ks_dd, (long)b * D, L.o.b, L.lnx.w, L.lnx.b, e->h, b, D,
+                                  EPS),
              "add+ln");
         // the cross-attention projects its own query from the layer-norm output
-        PROF(MZ_K_DEC_CROSS,
-             attn(nullptr, 0, L.xq.w, L.xq.b, xkv + (size_t)(2 * i) * nh * blk, xkv + (size_t)(2 * i + 1) * nh * blk,
-                  (long)nl * 2 * nh * blk, TENC, e->aslot + (size_t)i * nh),
-             "cross attention");
+        {
+            MzDecCross c{};
+            c.xin = e->h;
+            c.wq = L.xq.w;
+            c.qbias = L.xq.b;
+            c.k = xkv + (size_t)(2 * i) * nh * blk;
+            c.v = xkv + (size_t)(2 * i + 1) * nh * blk;
+            c.kv_b = (long)nl * 2 * nh * blk;
+            c.kv_h = blk;
+            c.ctr = e->ctr;
+            c.done = e->done;
+            c.out = e->datt;
+            c.B = b;
+            c.nh = nh;
+            c.d = D;
+            c.maxT = mt;
+            c.aslot = e->aslot + (size_t)i * nh;
+            c.align = e->align;
+            c.na = e->na;
+            PROF(MZ_K_DEC_CROSS, mz_dec_cross_launch(s, c), "cross attention");
+        }
         PROF(MZ_K_DEC_XO, gemm(DEPI_PARTIAL, e->datt, D, L.xo, D, D, ks_dd, e->part, D), "dec cross out-proj");
         PROF(MZ_K_DEC_ADDLN,
-             mz_dec_add_ln_launch(s, e->x, e->part, ks_dd, (long)b * D, L.xo.b, L.ln3.w, L.ln3.b, e->h, b, D, EPS),
+             mz_dec_add_ln_launch(s, e->x, e->x, e->part, ks_dd, (long)b * D, L.xo.b, L.ln3.w, L.ln3.b, e->h, b, D,
+                                  EPS),
              "add+ln");
         PROF(MZ_K_DEC_FC1, gemm(DEPI_GELU_F16, e->h, D, L.fc1, F, D, 1, e->dff, F), "dec fc1");
         PROF(MZ_K_DEC_FC2, gemm(DEPI_PARTIAL, e->dff, F, L.fc2, D, F, ks_df, e->part, D), "dec fc2");
         const Ln& nx = i + 1 < nl ? e->decv[i + 1].ln1 : e->dln;
         PROF(MZ_K_DEC_ADDLN,
-             mz_dec_add_ln_launch(s, e->x, e->part, ks_df, (long)b * D, L.fc2.b, nx.w, nx.b, e->h, b, D, EPS),
+             mz_dec_add_ln_launch(s, e->x, e->x, e->part, ks_df, (long)b * D, L.fc2.b, nx.w, nx.b, e->h, b, D, EPS),
              "add+ln");
         if (dtr) TRY(dtrace(i + 1), "decoder trace");
     }

@@ -58,7 +58,7 @@ __device__ __forceinline__ void ln_row4(float4 v, bool on, int dim, f16x4 wv, f1
 
 // ---------------------------------------------------------------- row kernels (one workgroup per row)
 
-__global__ void __launch_bounds__(512) dec_add_ln_kernel(float* __restrict__ x, const float* __restrict__ parts,
+__global__ void __launch_bounds__(512) dec_add_ln_kernel(const float* xin, float* x, const float* __restrict__ parts,
                                                          int nparts, long part_stride, const f16* __restrict__ bias,
                                                          const f16* __restrict__ w, const f16* __restrict__ b,
                                                          f16* __restrict__ y, int dim, float eps) {
@@ -74,7 +74,7 @@ __global__ void __launch_bounds__(512) dec_add_ln_kernel(float* __restrict__ x, 
 #pragma unroll
         for (int s = 0; s < MZ_MAX_PARTS; s++)
             if (s < nparts) pp[s] = *(const float4*)(parts + s * part_stride + idx);
-        v = *(const float4*)(x + idx);
+        v = *(const float4*)(xin + idx);
         const f16x4 bb = bias ? *(const f16x4*)(bias + c) : f16x4{};
         wv = *(const f16x4*)(w + c);
         bv = *(const f16x4*)(b + c);
@@ -558,6 +558,203 @@ __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
     for (int j = tid; j < L; j += blockDim.x) al[j] = __builtin_amdgcn_exp2f(sc[j] - M) * inv;
 }
 
+// ---------------------------------------------------------------- cross-attention for small batches
+
+// s_waitcnt operand that waits until at most n vector memory operations of this wave are outstanding (n < 64)
+constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// dec_attn_kernel<32, 8, true>'s arithmetic for batches of at most 256 / nh rows, where every (row, head) workgroup
+// has a CU to itself: with only B x nh workgroups streaming, one workgroup's bytes in flight set the rate (a
+// workgroup of the 32-row kernel keeps one batch, 64 KB, in flight). Here the row, all 64 query rows of wq (160
+// registers per lane) and batch 0 are requested together, and batches 1 and 2 straight into LDS (buffer_load ...
+// lds): ~350 KB in flight from the start, and the query projection waits only for its own operands (vmcnt counts
+// in issue order, so they are issued first). Then batches 3 (registers), 4 and 5 (refilling the two LDS slots as they
+// are read) follow. Same groups, key order, per-batch online-softmax updates, projection order and merge as
+// dec_attn_kernel: the same bits.
+__global__ void __launch_bounds__(256, 1) dec_cross_wide_kernel(const MzDecCross a) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    constexpr int AG = 32, AU = 8, BK = AG * AU, NB = (MZ_TENC + BK - 1) / BK, L = MZ_TENC;
+    static_assert(NB == 6, "the staging schedule below is written for 6 batches");
+    constexpr int NJ = MZ_DEC_KSLICE / 64;
+    __shared__ __attribute__((aligned(16))) f16x8 kvs[2][2][AU][256];  // [slot][k|v][key u][thread]
+    __shared__ __attribute__((aligned(16))) f16 xs[MZ_DEC_KSLICE];
+    __shared__ float qs[MZ_HD];
+    __shared__ float sc[MZ_TPAD];
+    __shared__ float gm[AG], gl[AG];
+    __shared__ float gacc[AG][MZ_HD + 1];
+    __shared__ float tot[2];
+
+    const int bh = blockIdx.x, b = bh / a.nh, head = bh - b * a.nh;
+    const int tid = threadIdx.x, grp = tid >> 3, sub = tid & 7, wave = tid >> 6;
+    const int r8 = (tid >> 3) & 7, q8 = tid & 7, nj = a.d >> 6;
+    // scalars first (scalar loads, waited for only where used)
+    const int pos = a.ctr[1];
+    const int slot = a.aslot ? a.aslot[head] : -1;
+    const bool done = a.done[b] != 0;
+    const f16* kb = a.k + (long)b * a.kv_b + (long)head * a.kv_h;
+    const f16* vb = a.v + (long)b * a.kv_b + (long)head * a.kv_h;
+    const __amdgpu_buffer_rsrc_t rK = rsrc(kb, L * MZ_HD * 2), rV = rsrc(vb, L * MZ_HD * 2);
+    f16x8 kk[AU], vv[AU];
+    auto fetch = [&](int i) {  // batch i of this group into registers
+#pragma unroll
+        for (int u = 0; u < AU; u++) {
+            const int j = i * BK + grp + u * AG;
+            kk[u] = j < L ? __builtin_nontemporal_load((const f16x8*)(kb + (long)j * MZ_HD + sub * 8)) : f16x8{};
+            vv[u] = j < L ? __builtin_nontemporal_load((const f16x8*)(vb + (long)j * MZ_HD + sub * 8)) : f16x8{};
+        }
+    };
+    // batch i of every group into LDS slot s_: 2 AU loads per wave, lane l of wave w writing the 16 bytes thread
+    // 64 w + l reads back; keys past L read zeros through the range check
+    auto stage = [&](int i, int s_) {
+#pragma unroll
+        for (int u = 0; u < AU; u++) {
+            const unsigned o = (unsigned)((i * BK + grp + u * AG) * MZ_HD + sub * 8) * 2u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rK, LDSP(&kvs[s_][0][u][wave * 64]), 16, o, 0, 0, MZ_NT);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rV, LDSP(&kvs[s_][1][u][wave * 64]), 16, o, 0, 0, MZ_NT);
+        }
+    };
+
+    // in issue order: the row (one 16-byte chunk per thread), this thread's 40 chunks of wq (rows 8 w + r8 and
+    // 32 + 8 w + r8, chunks q8, q8 + 8, ... of each), its two query biases, batch 0, batches 1 and 2 into LDS
+    const bool xl = tid < (a.d >> 3);
+    const f16x8 xv0 = xl ? *(const f16x8*)(a.xin + (long)b * a.d + tid * 8) : f16x8{};
+    const f16* wr = a.wq + (long)(head * MZ_HD + 8 * wave + r8) * a.d + q8 * 8;
+    f16x8 wv[2][NJ];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) wv[h][j] = j < nj ? *(const f16x8*)(wr + 32L * h * a.d + j * 64) : f16x8{};
+    const __amdgpu_buffer_rsrc_t rQB = rsrc(a.qbias, a.qbias ? (unsigned)a.d * 2u : 0u);
+    const unsigned short qb[2] = {__builtin_amdgcn_raw_buffer_load_b16(rQB, (unsigned)(head * MZ_HD + 8 * wave + r8) * 2u, 0, 0),
+                         __builtin_amdgcn_raw_buffer_load_b16(rQB, (unsigned)(head * MZ_HD + 32 + 8 * wave + r8) * 2u,
+                                                              0, 0)};
+    fetch(0);
+    stage(1, 0);
+    stage(2, 1);
+    __builtin_amdgcn_sched_barrier(0);  // every request above is issued before anything waits for data
+    if (done) {  // a finished row: no attention (the staged loads land before the LDS is released)
+        __builtin_amdgcn_s_waitcnt(vm_wait(0));
+        return;
+    }
+    if (xl) *(f16x8*)&xs[tid * 8] = xv0;
+    lds_barrier();  // the row in LDS; wq, the biases and the stream stay in flight
+
+    // q[i] = xin[b] . wq[head * 64 + i] + qbias, the two halves of rows in the order of dec_attn_kernel
+    constexpr float QS = 0.125f * 1.4426950408889634f;  // 1/8 and log2(e)
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        float t = 0.f;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            if (j < nj) {
+                const f16x8 xq = *(const f16x8*)&xs[(q8 + 8 * j) * 8];
+#pragma unroll
+                for (int e = 0; e < 8; e += 2)
+                    t = __builtin_amdgcn_fdot2(f16x2{wv[h][j][e], wv[h][j][e + 1]}, f16x2{xq[e], xq[e + 1]}, t, false);
+            }
+        }
+        t = group8_sum(t);
+        const int i = 32 * h + 8 * wave + r8;
+        if (q8 == 0) qs[i] = (t + (a.qbias ? (float)__builtin_bit_cast(f16, qb[h]) : 0.f)) * QS;
+    }
+    lds_barrier();
+    float q8v[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) q8v[e] = qs[sub * 8 + e];
+
+    float m = -INFINITY, l = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](int i, const f16x8(&K)[AU], const f16x8(&V)[AU]) {
+        const int j0 = i * BK + grp;
+        float s[AU];
+#pragma unroll
+        for (int u = 0; u < AU; u++) {
+            float t = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) t = fmaf(q8v[e], (float)K[u][e], t);
+            t = group8_sum(t);
+            const int j = j0 + u * AG;
+            s[u] = j < L ? t : -INFINITY;
+            if (slot >= 0 && sub == 0 && j < L) sc[j] = t;
+        }
+        float mx = s[0];  // key j0 < L: finite
+#pragma unroll
+        for (int u = 1; u < AU; u++) mx = fmaxf(mx, s[u]);
+        const float mn = fmaxf(m, mx);
+        const float cr = __builtin_amdgcn_exp2f(m - mn);
+        l *= cr;
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[e] *= cr;
+#pragma unroll
+        for (int u = 0; u < AU; u++) {
+            const float pe = __builtin_amdgcn_exp2f(s[u] - mn);
+            l += pe;
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[e] = fmaf(pe, (float)V[u][e], acc[e]);
+        }
+        m = mn;
+    };
+    // a slot's keys into (K, V) once its staged loads have landed (this wave's: the vmcnt wait before the call;
+    // every wave's: the barrier)
+    auto unstage = [&](int s_, f16x8(&K)[AU], f16x8(&V)[AU]) {
+        lds_barrier();
+#pragma unroll
+        for (int u = 0; u < AU; u++) {
+            K[u] = kvs[s_][0][u][tid];
+            V[u] = kvs[s_][1][u][tid];
+        }
+    };
+    // batches 0, 3 in registers; 1, 4 through slot 0; 2, 5 through slot 1 (2 AU vector memory operations per batch)
+    f16x8 ks[AU], vs[AU];
+    compute(0, kk, vv);
+    fetch(3);
+    __builtin_amdgcn_s_waitcnt(vm_wait(2 * AU));  // all but batch 3: batches 1 and 2 have landed
+    unstage(0, ks, vs);
+    lds_barrier();  // every wave has read slot 0
+    stage(4, 0);
+    compute(1, ks, vs);
+    __builtin_amdgcn_s_waitcnt(vm_wait(4 * AU));  // all but batches 3 and 4
+    unstage(1, ks, vs);
+    lds_barrier();
+    stage(5, 1);
+    compute(2, ks, vs);
+    compute(3, kk, vv);
+    __builtin_amdgcn_s_waitcnt(vm_wait(2 * AU));  // all but batch 5
+    unstage(0, ks, vs);
+    compute(4, ks, vs);
+    __builtin_amdgcn_s_waitcnt(vm_wait(0));
+    unstage(1, ks, vs);
+    compute(5, ks, vs);
+
+    if (sub == 0) {
+        gm[grp] = m;
+        gl[grp] = l;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) gacc[grp][sub * 8 + e] = acc[e];
+    __syncthreads();
+    if (tid < MZ_HD) {
+        float M = gm[0];
+        for (int g = 1; g < AG; g++) M = fmaxf(M, gm[g]);
+        float lt = 0.f, o = 0.f;
+        for (int g = 0; g < AG; g++) {
+            const float w = __builtin_amdgcn_exp2f(gm[g] - M);
+            lt = fmaf(gl[g], w, lt);
+            o = fmaf(gacc[g][tid], w, o);
+        }
+        a.out[(long)b * a.d + head * MZ_HD + tid] = (f16)(o / lt);
+        if (tid == 0) {
+            tot[0] = M;
+            tot[1] = lt;
+        }
+    }
+    if (slot < 0 || pos >= a.maxT) return;
+    __syncthreads();
+    const float M = tot[0], inv = 1.f / tot[1];
+    float* al = a.align + (((long)b * a.maxT + pos) * a.na + slot) * MZ_TENC;
+    for (int j = tid; j < L; j += 256) al[j] = __builtin_amdgcn_exp2f(sc[j] - M) * inv;
+#endif
+}
+
 // ---------------------------------------------------------------- greedy choice
 
 // Token p + 1 of row b from the LM head's per-workgroup partials (value, id) (kernels/whisper.cu:451-493 rules:
@@ -662,13 +859,45 @@ hipError_t mz_dec_attn_launch(hipStream_t s, const MzDecAttn& a) {
     return hipGetLastError();
 }
 
+hipError_t mz_dec_cross_launch(hipStream_t s, const MzDecCross& a) {
+    if (a.maxT <= 0 || a.B <= 0 || a.nh <= 0 || a.d % 64 != 0 || a.d > MZ_DEC_KSLICE || a.d != a.nh * MZ_HD || !a.xin ||
+        !a.wq)
+        return hipErrorInvalidValue;
+    if (a.aslot && (!a.align || a.na <= 0)) return hipErrorInvalidValue;
+    if (a.B * a.nh <= 256) {  // one workgroup per CU, all at once
+        hipLaunchKernelGGL(dec_cross_wide_kernel, dim3(a.B * a.nh), dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
+    MzDecAttn c{};
+    c.qbias = a.qbias;
+    c.xin = a.xin;
+    c.wq = a.wq;
+    c.k = a.k;
+    c.v = a.v;
+    c.kv_b = a.kv_b;
+    c.kv_h = a.kv_h;
+    c.L = MZ_TENC;
+    c.ctr = a.ctr;
+    c.done = a.done;
+    c.out = a.out;
+    c.B = a.B;
+    c.nh = a.nh;
+    c.d = a.d;
+    c.maxT = a.maxT;
+    c.aslot = a.aslot;
+    c.align = a.align;
+    c.na = a.na;
+    return mz_dec_attn_launch(s, c);
+}
+
 static int row_threads(int dim) { return (dim / 4 + 63) / 64 * 64; }
 
-hipError_t mz_dec_add_ln_launch(hipStream_t s, float* x, const float* parts, int nparts, long part_stride,
-                                const f16* bias, const f16* w, const f16* b, f16* y, int rows, int dim, float eps) {
+hipError_t mz_dec_add_ln_launch(hipStream_t s, const float* xin, float* x, const float* parts, int nparts,
+                                long part_stride, const f16* bias, const f16* w, const f16* b, f16* y, int rows,
+                                int dim, float eps) {
     if (dim % 4 != 0 || dim > 2048 || rows <= 0 || nparts < 0 || nparts > MZ_MAX_PARTS) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(dec_add_ln_kernel, dim3(rows), dim3(row_threads(dim)), 0, s, x, parts, nparts, part_stride, bias,
-                       w, b, y, dim, eps);
+    hipLaunchKernelGGL(dec_add_ln_kernel, dim3(rows), dim3(row_threads(dim)), 0, s, xin, x, parts, nparts, part_stride,
+                       bias, w, b, y, dim, eps);
     return hipGetLastError();
 }
 

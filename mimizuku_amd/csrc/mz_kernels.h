@@ -121,9 +121,32 @@ struct MzDecAttn {
 };
 hipError_t mz_dec_attn_launch(hipStream_t s, const MzDecAttn& a);
 
-// x[b] += sum_s parts[s][b] + bias; y[b] = LN(x[b])  (the residual add fused with the next layer norm)
-hipError_t mz_dec_add_ln_launch(hipStream_t s, float* x, const float* parts, int nparts, long part_stride,
-                                const f16* bias, const f16* w, const f16* b, f16* y, int rows, int dim, float eps);
+// Cross-attention of one query per (row, head) over the encoder's 1500 keys with its own query projection
+// (kernels/whisper.cu:355-449, 309-317): q = wq[head rows] . xin[b] + qbias, xin the row's LayerNorm output. The keys
+// and values of (b, head) are 1500 rows of 64 halves at k + b * kv_b + head * kv_h (v likewise). Batches of at most
+// 256 / nh rows run a variant that keeps more of each workgroup's stream in flight; both give the same bits.
+struct MzDecCross {
+    const f16* xin;  // [B][d]
+    const f16* wq;   // [d][d], row = output feature
+    const f16* qbias;
+    const f16* k;
+    const f16* v;
+    long kv_b, kv_h;
+    const int* ctr;
+    const int* done;
+    f16* out;        // [B][d]
+    int B, nh, d, maxT;
+    const int* aslot;  // alignment slot of each head of this layer or -1 (may be null)
+    float* align;      // [bmax][maxT][na][1500]
+    int na;
+};
+hipError_t mz_dec_cross_launch(hipStream_t s, const MzDecCross& a);
+
+// x[b] = xin[b] + sum_s parts[s][b] + bias; y[b] = LN(x[b])  (the residual add fused with the next layer norm;
+// xin may be x)
+hipError_t mz_dec_add_ln_launch(hipStream_t s, const float* xin, float* x, const float* parts, int nparts,
+                                long part_stride, const f16* bias, const f16* w, const f16* b, f16* y, int rows,
+                                int dim, float eps);
 // ctr[1] = ctr[0]; x[b] = emb[tok[b * maxT + p]] + pe[p] (fp32); y[b] = LN(x[b])
 hipError_t mz_dec_embed_ln_launch(hipStream_t s, const int* tok, int* ctr, const f16* emb, const f16* pe, float* x,
                                   const f16* w, const f16* b, f16* y, int rows, int dim, int maxT, float eps);

@@ -236,3 +236,37 @@ def test_graph_replay_at_position_200_equals_eager():
           eager[0][:4, npr:].tolist(), "...")
     e.close()
     ctx.close()
+
+
+def test_cross_attention_variants_give_the_same_bits():
+    """The cross-attention runs as one of two variants chosen by the batch: at most 12 rows (one workgroup per CU, two
+    batches of keys staged in LDS) or more (three workgroups per CU, half a batch staged). Where the keys come from
+    does not change the arithmetic: the same 12 rows stepped in a batch of 32 and in a batch of 12 give the same bits
+    (tokens, logits, alignment rows, residual stream), greedy from a 4-token prompt through 6 positions."""
+    rng = np.random.default_rng(24)
+    W = synth.random_weights(G, seed=9, bias_std=0.02, ln_std=0.1)
+    gen = synth.generation_config(G, align_heads=[[2, 4], [2, 11], [3, 3], [3, 6], [3, 11], [3, 14]])
+    dims = model.Dims(G.d, G.ff, G.nh, G.enc_layers, G.dec_layers, G.n_mels, G.vocab, G.max_t)
+    gc = model.GenCfg.from_dict(gen, dims)
+    xkv = np.zeros((B, G.dec_layers, 2, G.nh, TPAD, 64), np.float16)
+    for b in range(B):
+        xkv[b, :, :, :, :1500] = rng.standard_normal((G.dec_layers, 2, G.nh, 1500, 64), dtype=np.float32)
+    npr, steps, few = 4, 10, 12
+    prompts = rng.integers(0, 50000, size=(B, npr)).astype(np.int32)
+    ctx = model.Context(0)
+    e = model.Engine(ctx, dims, gc, B, 8)
+    e.load(W)
+    p, _ = e.buffer(L.BUF_XKV)
+    ctx.upload(p, xkv)
+    del xkv
+    out = {}
+    for nb in (B, few):
+        e.reset(prompts[:nb])
+        for _ in range(steps):
+            e.step(nb, False, npr)
+        out[nb] = (e.tokens()[:few, :steps + 1], e.logits()[:few], e.align()[:few, :steps], e.dec_x()[:few])
+    for n, a, g in zip(("tokens", "logits", "alignment rows", "residual"), out[B], out[few]):
+        np.testing.assert_array_equal(a, g, err_msg=n)
+    print("cross-attention variants: 12 rows in a batch of 32 and alone give the same bits over", steps, "steps")
+    e.close()
+    ctx.close()
