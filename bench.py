@@ -126,10 +126,16 @@ def probe(name: str, reps: int = 5):
         return (rng.standard_normal(shape, dtype=np.float32) * sc).astype(np.float16)
 
     name_graph = name == "dec_graph"
+    rows = N_CLIPS
+    if name.startswith("dec_step_b"):  # the same decoder-step probe with fewer rows (dec_step_b8, dec_step_b1)
+        rows = int(name[len("dec_step_b"):])
+        if not 1 <= rows <= N_CLIPS:
+            raise SystemExit(f"probe {name}: 1 to {N_CLIPS} rows")
+        name = "dec_step"
     if name in ("dec_step", "dec_graph"):
-        # three eager turbo decoder steps at B = 32 from position 200 (random self cache and cross keys/values):
-        # the decoder kernels at the benchmark's step shape, one dispatch each per layer and step ("dec_graph":
-        # twenty replays of the captured step instead)
+        # three eager turbo decoder steps at B = 32 (or `rows`) from position 200 (random self cache and cross
+        # keys/values): the decoder kernels at the benchmark's step shape, one dispatch each per layer and step
+        # ("dec_graph": twenty replays of the captured step instead)
         gd = synth.Geometry(d=d, ff=ff, nh=nh, enc_layers=1, dec_layers=g.dec_layers, n_mels=g.n_mels, vocab=g.vocab)
         W = synth.random_weights(gd, seed=0)
         gen = synth.generation_config(gd, align_heads=synth.generation_config(g)["alignment_heads"])
@@ -146,15 +152,15 @@ def probe(name: str, reps: int = 5):
         ctx.upload(e.buffer(L.BUF_TOK)[0], toks)
         ctx.upload(e.buffer(L.BUF_CTR)[0], np.array([200, 0, 0, 0], np.int32))
         if name_graph:  # the captured step replayed 20 times (the benchmark's own launch path)
-            e.capture(N_CLIPS, 1)
+            e.capture(rows, 1)
             for _ in range(20):
                 e.replay()
         else:
             for _ in range(3):
-                e.step(N_CLIPS, False, 1)
+                e.step(rows, False, 1)
         ctx.sync()
-        print(json.dumps({"probe": name, "steps": 20 if name_graph else 3, "position": 200,
-                          "dec_cross_bytes": dec_kernel_bytes(g, N_CLIPS, 201, 6)["dec_cross"]}))
+        print(json.dumps({"probe": name, "rows": rows, "steps": 20 if name_graph else 3, "position": 200,
+                          "dec_cross_bytes": dec_kernel_bytes(g, rows, 201, 6)["dec_cross"]}))
         e.close()
         return
     if name == "copy":
