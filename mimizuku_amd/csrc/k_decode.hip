@@ -125,6 +125,10 @@ __global__ void __launch_bounds__(512) dec_embed_ln_kernel(const int* __restrict
 typedef __attribute__((address_space(3))) void lds_void;
 #define LDSP(q) ((lds_void*)(q))
 
+// s_waitcnt operand that waits until at most n vector memory operations of this wave are outstanding (n < 64)
+constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+
 constexpr int MZ_NT = 2;  // cache-policy bit of a buffer load: nontemporal (weights are streamed once per step)
 
 // One workgroup per (32 output columns, K slice, 32 rows): both operands of its K slice (<= MZ_DEC_KSLICE) go from
@@ -236,7 +240,7 @@ __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
         }
         const float a = v[e] + bv[e];
         if (EPI == DEPI_GELU_F16) {
-            ((f16*)p.out)[(long)m * p.ldo + n] = (f16)gelu_erf(a);
+            ((f16*)p.out)[(long)m * p.ldo + n] = (f16)gelu_erf_h(a);
         } else if (EPI == DEPI_F16) {
             ((f16*)p.out)[(long)m * p.ldo + n] = (f16)a;
         }
@@ -408,11 +412,22 @@ __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
     __shared__ __attribute__((aligned(16))) f16 kvn[2][MZ_HD];  // the step's own key and value (self, kw set)
 
     const int bh = blockIdx.x, b = bh / a.nh, head = bh - b * a.nh;
-    if (a.done[b]) return;
     const int tid = threadIdx.x, grp = tid >> 3, sub = tid & 7;
-    const int pos = a.ctr[1];
-    const int L = a.L > 0 ? a.L : min(pos + 1, a.maxT);
-    const int slot = CROSS && a.aslot ? a.aslot[head] : -1;
+    // the row's done flag, the position and the alignment slot: the self-attention reads them first (its keys'
+    // count needs the position); the cross-attention (L given), whose keys do not depend on the step, once its
+    // first requests are issued
+    bool done = false;
+    int pos = 0, slot = -1;
+    auto step_scalars = [&] {
+        done = a.done[b] != 0;
+        pos = a.ctr[1];
+        slot = CROSS && a.aslot ? a.aslot[head] : -1;
+    };
+    if (!CROSS) {
+        step_scalars();
+        if (done) return;
+    }
+    const int L = CROSS ? a.L : min(pos + 1, a.maxT);
 
     // the first batch of keys and values is requested before the query, which arrives in the same round trip
     const f16* kb = a.k + (long)b * a.kv_b + (long)head * a.kv_h + sub * 8;
@@ -433,15 +448,34 @@ __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
         // 16-byte chunks q8, q8 + 8, ... of each (nj per row); 8 lanes sum one row through DPP
         const int w = tid >> 6, r8 = (tid >> 3) & 7, q8 = tid & 7, nj = a.d >> 6;
         constexpr int NJ = MZ_DEC_KSLICE / 64;
-        const f16* wr = a.wq + (long)(head * MZ_HD + 8 * w + r8) * a.d + q8 * 8;
-        // in issue order: the row (one chunk per thread, d / 8 <= 160), the first 32 weight rows, the first keys and
-        // values; each wait below then covers only what it needs
+        // in issue order, with no wait between them (range-checked buffer loads, zeros past the range, so no load
+        // sits behind a branch): the row (one chunk per thread, d / 8 <= 160), the first 32 weight rows, this
+        // thread's two query biases, the first keys and values; each wait below then covers only what it needs.
+        // Chunks j >= nj of a weight row read the next row or zeros and are never used.
         const bool xl = tid < (a.d >> 3);
-        const f16x8 xv0 = xl ? *(const f16x8*)(a.xin + (long)b * a.d + tid * 8) : f16x8{};
+        const __amdgpu_buffer_rsrc_t rX = rsrc(a.xin + (long)b * a.d, (unsigned)a.d * 2u);
+        const __amdgpu_buffer_rsrc_t rW = rsrc(a.wq + (long)head * MZ_HD * a.d, (unsigned)(MZ_HD * a.d) * 2u);
+        const __amdgpu_buffer_rsrc_t rQB = rsrc(a.qbias, a.qbias ? (unsigned)a.d * 2u : 0u);
+        const unsigned wo = (unsigned)(((8 * w + r8) * a.d + q8 * 8) * 2);
+        const f16x8 xv0 = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rX, (unsigned)tid * 16u, 0, 0));
         f16x8 wv[NJ];
 #pragma unroll
-        for (int j = 0; j < NJ; j++) wv[j] = j < nj ? *(const f16x8*)(wr + j * 64) : f16x8{};
-        fetch(grp);
+        for (int j = 0; j < NJ; j++)
+            wv[j] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rW, wo + j * 128u, 0, 0));
+        const unsigned short qb[2] = {
+            __builtin_amdgcn_raw_buffer_load_b16(rQB, (unsigned)(head * MZ_HD + 8 * w + r8) * 2u, 0, 0),
+            __builtin_amdgcn_raw_buffer_load_b16(rQB, (unsigned)(head * MZ_HD + 32 + 8 * w + r8) * 2u, 0, 0)};
+#pragma unroll
+        for (int u = 0; u < AU; u++) {  // the first batch: keys grp + 32 u < 256 <= L (checked at launch)
+            kk[u] = __builtin_nontemporal_load((const f16x8*)(kb + (long)(grp + u * AG) * MZ_HD));
+            vv[u] = __builtin_nontemporal_load((const f16x8*)(vb + (long)(grp + u * AG) * MZ_HD));
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every request above is issued before anything waits for data
+        step_scalars();
+        if (done) {  // a finished row: no attention
+            __builtin_amdgcn_s_waitcnt(vm_wait(0));
+            return;
+        }
         if (xl) *(f16x8*)&xs[tid * 8] = xv0;
         lds_barrier();  // the row in LDS; the weight rows, keys and values stay in flight
 #pragma unroll
@@ -458,13 +492,17 @@ __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
             }
             if (half == 0) {  // the second 32 rows, requested once the first ones are consumed
 #pragma unroll
-                for (int j = 0; j < NJ; j++) wv[j] = j < nj ? *(const f16x8*)(wr + 32L * a.d + j * 64) : f16x8{};
+                for (int j = 0; j < NJ; j++)
+                    wv[j] = __builtin_bit_cast(
+                        f16x8, __builtin_amdgcn_raw_buffer_load_b128(rW, wo + (unsigned)(32 * a.d * 2) + j * 128u, 0, 0));
             }
             t = group8_sum(t);
             const int i = 32 * half + 8 * w + r8;
-            if (q8 == 0) qs[i] = (t + (a.qbias ? (float)a.qbias[head * MZ_HD + i] : 0.f)) * QS;
+            if (q8 == 0) qs[i] = (t + (a.qbias ? (float)__builtin_bit_cast(f16, qb[half]) : 0.f)) * QS;
         }
     } else {
+        if (CROSS) step_scalars();  // (the cross-attention without its query projection)
+        if (done) return;
         fetch(grp);
         // thread 64 w + i takes dim i of q (w = 0) or, with kw set, of the step's key (1) or value (2)
         const long qrow = a.qrow ? a.qrow : a.d;
@@ -559,9 +597,6 @@ __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
 }
 
 // ---------------------------------------------------------------- cross-attention for small batches
-
-// s_waitcnt operand that waits until at most n vector memory operations of this wave are outstanding (n < 64)
-constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 // dec_attn_kernel<32, 8, true>'s arithmetic for batches of at most 256 / nh rows, where every (row, head) workgroup
 // has a CU to itself: with only B x nh workgroups streaming, one workgroup's bytes in flight set the rate (a
@@ -850,7 +885,8 @@ hipError_t mz_dec_attn_launch(hipStream_t s, const MzDecAttn& a) {
     if (a.maxT <= 0 || a.B <= 0 || a.nh <= 0 || a.L > MZ_TPAD || (a.L <= 0 && a.maxT > MZ_TPAD)) return hipErrorInvalidValue;
     if (a.aslot && (!a.align || a.na <= 0 || (a.L > 0 && a.L != MZ_TENC))) return hipErrorInvalidValue;
     // the fused query projection: cross-attention only, whole 64-half chunks per lane group, the row in LDS
-    if (a.wq && (a.L <= 0 || !a.xin || a.d % 64 != 0 || a.d > MZ_DEC_KSLICE)) return hipErrorInvalidValue;
+    // (and at least one whole first batch of keys, L >= 256, which the kernel requests without a range check)
+    if (a.wq && (a.L < 32 * 8 || !a.xin || a.d % 64 != 0 || a.d > MZ_DEC_KSLICE)) return hipErrorInvalidValue;
     // two instances (the query projection compiled only into the cross one), also told apart by name in traces
     if (a.L > 0)
         hipLaunchKernelGGL((dec_attn_kernel<32, 8, true>), dim3(a.B * a.nh), dim3(32 * 8), 0, s, a);

@@ -280,7 +280,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
             if (EPI == EPI_F16) {
                 __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (f16)v), rO, o, 0, 0);
             } else if (EPI == EPI_GELU_F16) {
-                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (f16)gelu_erf(v)), rO, o, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (f16)gelu_erf_h(v)), rO, o, 0, 0);
             } else {
                 const float x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rO, o, 0, 0));
                 __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, x + v), rO, o, 0, 0);

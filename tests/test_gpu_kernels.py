@@ -215,9 +215,10 @@ def test_gemm_epilogues(ctx):
 def test_gemm_gelu_every_fp16_value(ctx):
     """The GELU epilogue on every finite fp16 input: row m of x holds value m in column 0 and w is 1 there, so each
     accumulator is exactly that value; no bias (a missing bias reads zeros). Against 0.5 v erfc(-v / sqrt 2) in float64:
-    within 1.5 fp16 ulp everywhere (the Abramowitz & Stegun erf reaches 1.28 in the tail, at v = -4.08) and correctly
-    rounded for all but a few hundred values (257 measured). Every column of a row is the same value, and the 64 columns
-    cover both the whole-block and the column-checked stores."""
+    within 0.6 fp16 ulp everywhere (0.505 measured, at v = 0.0036; an emulation of the fp32 arithmetic on the host
+    gives the same, with exp2 correctly rounded or one ulp off) and correctly rounded for all but a few hundred values
+    (164 measured; 157-171 in the emulation). Every column of a row is the same value, and the 64 columns cover both
+    the whole-block and the column-checked stores."""
     from scipy.special import erfc
     v = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
     v = v[np.isfinite(v)]
@@ -244,9 +245,9 @@ def test_gemm_gelu_every_fp16_value(ctx):
     worst = int(np.argmax(err))
     print("GELU over %d fp16 values: max %.3f ulp at v = %g; %d not correctly rounded" %
           (v.size, err[worst], vd[worst], int((y[:, 0] != ref.astype(np.float16)).sum())))
-    assert err[~sub].max() <= 1.5, ("normal inputs", vd[~sub][np.argmax(err[~sub])])
-    assert err[sub].max() <= 1.5, ("subnormal inputs", vd[sub][np.argmax(err[sub])])
-    assert (y[:, 0] != ref.astype(np.float16)).sum() < 1000
+    assert err[~sub].max() <= 0.6, ("normal inputs", vd[~sub][np.argmax(err[~sub])])
+    assert err[sub].max() <= 0.6, ("subnormal inputs", vd[sub][np.argmax(err[sub])])
+    assert (y[:, 0] != ref.astype(np.float16)).sum() < 300
 
 
 @pytest.mark.parametrize("kind", [3, 2])
