@@ -223,6 +223,9 @@ int mz_engine_profile_read(mz_engine* e, int kernel, double* total_ms, int* coun
                              * layer and after the last one, of the last eager step (not recorded by graph replays) */
 #define MZ_BUF_SELF_K 11 /* f16 [dec_layers][bmax][nh][max_t][64] self-attention key cache */
 #define MZ_BUF_SELF_V 12 /* f16 [dec_layers][bmax][nh][max_t][64] self-attention value cache */
+#define MZ_BUF_ALIGN_H 13 /* f16 [bmax][max_t][n_align][1500]: MZ_BUF_ALIGN's rows rounded to fp16, written by the
+                           * same kernels; the reference's own align buffer (src/model.rs:455), which
+                           * src/transcribe.rs:158 reads with download_h */
 /* Device address and size of an engine buffer. */
 int mz_engine_buffer(mz_engine* e, int which, uint64_t* dptr, size_t* bytes);
 /* Synchronise, then copy bytes at byte offset `offset` of an engine buffer to host memory. */

@@ -43,7 +43,7 @@ class Times(C.Structure):
 
 EPI_F16, EPI_GELU_F16, EPI_RESID_F32, EPI_GELU_POS, EPI_HEADS = range(5)
 (BUF_TOK, BUF_DONE, BUF_CTR, BUF_ALIGN, BUF_ENC_OUT, BUF_LOGITS, BUF_TRACE, BUF_XKV, BUF_DEC_X, BUF_ENC_X,
- BUF_DEC_TRACE, BUF_SELF_K, BUF_SELF_V) = range(13)
+ BUF_DEC_TRACE, BUF_SELF_K, BUF_SELF_V, BUF_ALIGN_H) = range(14)
 DT_F16, DT_F32 = 0, 1
 # kernel classes of mz_engine_profile_read
 K_NAMES = ["mel", "conv1", "conv2", "ln", "qkv", "attn", "oproj", "fc1", "fc2", "xkv", "step",

@@ -152,6 +152,7 @@ struct mz_engine {
     float *x = nullptr, *part = nullptr, *logits = nullptr;
     f16 *h = nullptr, *datt = nullptr, *dff = nullptr, *kc = nullptr, *vc = nullptr;
     float* align = nullptr;  // alignment-head probabilities [bmax][max_t][na][1500], fp32
+    f16* alignh = nullptr;   // the same rows rounded to fp16 (the reference's own buffer, src/model.rs:455)
     int2* amax = nullptr;  // LM head argmax partials [mz_lm_blocks(vocab)][bmax]
     int* aslot = nullptr;
     unsigned char *sup = nullptr, *sup_lang = nullptr;
@@ -255,7 +256,7 @@ extern "C" size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int 
     size_t enc = G * d->n_mels * NFR * 4 + G * NFR * d->n_mels * 2 + G * NFR * D * 2 + G * TENC * D * 4 +
                  G * TENC * D * 2 * 3 + G * 3 * nh * TPAD * HD * 2 + G * TENC * F * 2;
     size_t dec = B * nl * 2 * nh * TPAD * HD * 2 + B * mt * 4 + B * 4 + 16 + B * D * 4 + B * D * 2 * 2 + B * F * 2 +
-                 2 * nl * B * nh * mt * HD * 2 + B * V * 4 + B * mt * n_align * TENC * 4 + (size_t)mz_lm_blocks((int)V) * B * 8 +
+                 2 * nl * B * nh * mt * HD * 2 + B * V * 4 + B * mt * n_align * TENC * (4 + 2) + (size_t)mz_lm_blocks((int)V) * B * 8 +
                  nl * nh * 4 + 2 * V;
     size_t part = part_elems((int)D, (int)F, (int)B) * 4;
     size_t ts = B * 8 + 2 * B * n_align * TENC * 4 + B * (size_t)mz_ts_diag_stride((int)mt - 1, TENC) * 5 + B * mt * 4;
@@ -420,6 +421,7 @@ extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, in
         (r = e->alloc(&e->dff, B * F)) || (r = e->alloc(&e->kc, (size_t)nl * B * nh * mt * HD)) ||
         (r = e->alloc(&e->vc, (size_t)nl * B * nh * mt * HD)) || (r = e->alloc(&e->logits, B * V)) ||
         (r = e->alloc(&e->align, B * mt * e->na * (size_t)TENC)) ||
+        (r = e->alloc(&e->alignh, B * mt * e->na * (size_t)TENC)) ||
         (r = e->alloc(&e->amax, (size_t)mz_lm_blocks(V) * B)) ||
         (r = e->alloc(&e->aslot, (size_t)nl * nh)) || (r = e->alloc(&e->sup, V)) || (r = e->alloc(&e->sup_lang, V)))
         return fail(r);
@@ -842,6 +844,7 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
             c.maxT = mt;
             c.aslot = e->aslot + (size_t)i * nh;
             c.align = e->align;
+            c.alignh = e->alignh;
             c.na = e->na;
             PROF(MZ_K_DEC_CROSS, mz_dec_cross_launch(s, c), "cross attention");
         }
@@ -948,6 +951,7 @@ extern "C" int mz_engine_buffer(mz_engine* e, int which, uint64_t* dptr, size_t*
         case MZ_BUF_DONE: p = e->done, n = B * 4; break;
         case MZ_BUF_CTR: p = e->ctr, n = 16; break;
         case MZ_BUF_ALIGN: p = e->align, n = B * mt * e->na * TENC * 4; break;
+        case MZ_BUF_ALIGN_H: p = e->alignh, n = B * mt * e->na * TENC * 2; break;
         case MZ_BUF_ENC_OUT: p = e->hb, n = G * TENC * D * 2; break;
         case MZ_BUF_LOGITS: p = e->logits, n = B * e->dm.vocab * 4; break;
         case MZ_BUF_TRACE:
@@ -1016,7 +1020,7 @@ extern "C" int mz_engine_free(mz_engine* e) {
     for (void* p : {(void*)e->arena, (void*)e->mel, (void*)e->melT, (void*)e->h1, (void*)e->ex, (void*)e->hb, (void*)e->dd,
                     (void*)e->qkvh, (void*)e->att, (void*)e->ff, (void*)e->trace, (void*)e->dtrace, (void*)e->xkvbuf, (void*)e->tok,
                     (void*)e->done, (void*)e->ctr, (void*)e->x, (void*)e->h, (void*)e->datt,
-                    (void*)e->dff, (void*)e->kc, (void*)e->vc, (void*)e->logits, (void*)e->align, (void*)e->amax,
+                    (void*)e->dff, (void*)e->kc, (void*)e->vc, (void*)e->logits, (void*)e->align, (void*)e->alignh, (void*)e->amax,
                     (void*)e->aslot, (void*)e->sup, (void*)e->sup_lang,
                     (void*)e->part})
         if (p) mz_free(e->c, (uint64_t)(uintptr_t)p);

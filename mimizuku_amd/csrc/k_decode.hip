@@ -592,8 +592,14 @@ __global__ void __launch_bounds__(AG * 8) dec_attn_kernel(const MzDecAttn a) {
     if (slot < 0 || pos >= a.maxT) return;
     __syncthreads();
     const float M = tot[0], inv = 1.f / tot[1];
-    float* al = a.align + (((long)b * a.maxT + pos) * a.na + slot) * MZ_TENC;
-    for (int j = tid; j < L; j += blockDim.x) al[j] = __builtin_amdgcn_exp2f(sc[j] - M) * inv;
+    const long ao = (((long)b * a.maxT + pos) * a.na + slot) * MZ_TENC;
+    float* al = a.align + ao;
+    f16* alh = a.alignh ? a.alignh + ao : nullptr;
+    for (int j = tid; j < L; j += blockDim.x) {
+        const float pj = __builtin_amdgcn_exp2f(sc[j] - M) * inv;
+        al[j] = pj;
+        if (alh) alh[j] = (f16)pj;
+    }
 }
 
 // ---------------------------------------------------------------- cross-attention for small batches
@@ -785,8 +791,14 @@ __global__ void __launch_bounds__(256, 1) dec_cross_wide_kernel(const MzDecCross
     if (slot < 0 || pos >= a.maxT) return;
     __syncthreads();
     const float M = tot[0], inv = 1.f / tot[1];
-    float* al = a.align + (((long)b * a.maxT + pos) * a.na + slot) * MZ_TENC;
-    for (int j = tid; j < L; j += 256) al[j] = __builtin_amdgcn_exp2f(sc[j] - M) * inv;
+    const long ao = (((long)b * a.maxT + pos) * a.na + slot) * MZ_TENC;
+    float* al = a.align + ao;
+    f16* alh = a.alignh ? a.alignh + ao : nullptr;
+    for (int j = tid; j < L; j += 256) {
+        const float pj = __builtin_amdgcn_exp2f(sc[j] - M) * inv;
+        al[j] = pj;
+        if (alh) alh[j] = (f16)pj;
+    }
 #endif
 }
 
@@ -922,6 +934,7 @@ hipError_t mz_dec_cross_launch(hipStream_t s, const MzDecCross& a) {
     c.maxT = a.maxT;
     c.aslot = a.aslot;
     c.align = a.align;
+    c.alignh = a.alignh;
     c.na = a.na;
     return mz_dec_attn_launch(s, c);
 }

@@ -117,6 +117,7 @@ struct MzDecAttn {
     // alignment-head capture (cross only, may be null): slot of each head of this layer or -1
     const int* aslot;
     float* align;      // [bmax][maxT][na][1500]
+    f16* alignh;       // the same rows rounded to fp16 (may be null)
     int na;
 };
 hipError_t mz_dec_attn_launch(hipStream_t s, const MzDecAttn& a);
@@ -138,6 +139,7 @@ struct MzDecCross {
     int B, nh, d, maxT;
     const int* aslot;  // alignment slot of each head of this layer or -1 (may be null)
     float* align;      // [bmax][maxT][na][1500]
+    f16* alignh;       // the same rows rounded to fp16 (may be null)
     int na;
 };
 hipError_t mz_dec_cross_launch(hipStream_t s, const MzDecCross& a);

@@ -21,6 +21,19 @@ def declared_functions():
     return sorted(set(re.findall(r"\b(mz_[a-z0-9_]+)\s*\(", text)))
 
 
+def test_header_constants_match_the_python_mirror():
+    """Every buffer id, epilogue, data type and kernel class that the header defines has the same value in the Python
+    mirror (a caller binding the header and these tests read the same buffers)."""
+    defs = {k: int(v) for k, v in re.findall(r"#define MZ_([A-Z0-9_]+)\s+(\d+)", open(HEADER).read())}
+    groups = [k for k in defs if k.startswith(("BUF_", "EPI_", "DT_"))]
+    assert len(groups) >= 14 + 5 + 2
+    for k in groups:
+        assert getattr(L, k) == defs[k], k
+    kinds = sorted((v, k) for k, v in defs.items() if k.startswith("K_"))
+    assert [v for v, _ in kinds] == list(range(len(L.K_NAMES)))
+    assert [k[2:].lower() for _, k in kinds] == L.K_NAMES
+
+
 def test_library_exports_every_declared_function():
     lib = L.lib()
     names = declared_functions()

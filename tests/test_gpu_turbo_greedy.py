@@ -9,7 +9,10 @@ at most 1e-2:
 * every generated token equals the oracle's greedy choice (src/model.rs:650-736, kernels/whisper.cu:451-493 rules);
 * every token's start time from the engine's alignment rows, computed on the device (the product's timestamp path),
   equals the one R.token_timestamps computes from the oracle's own cross-attention probabilities in the reference's
-  fp16 arithmetic (src/transcribe.rs:147-162, src/align.rs:8-106).
+  fp16 arithmetic (src/transcribe.rs:147-162, src/align.rs:8-106);
+* the fp16 alignment buffer (the reference's own, src/model.rs:455) holds the fp32 rows rounded to fp16, bit for bit,
+  and the times a reference caller computes from it (download_h, then align.rs) equal the oracle's from its
+  probabilities rounded to fp16.
 
 Alignment that DTW can resolve. With random weights and random cross keys the alignment heads' rows are nearly
 uniform (the largest probability ~0.01) and DTW on them is decided by differences at the level of the fp16 rounding
@@ -94,6 +97,10 @@ def test_greedy_tokens_and_timestamps_turbo_widths():
     ts_dev = transcribe.jump_times_device(ctx, ap + NP * na * TENC * 4, G.max_t * na * TENC, rows,
                                           np.full(B, TENC, np.int32), na, TENC, 7, True)
     al = e.align()[:B, NP:NP + GEN - 1].astype(np.float32)  # [B][rows][slots][1500]
+    # the fp16 rows of the reference's own buffer (src/model.rs:455): the fp32 rows rounded, bit for bit
+    ah = e.read(L.BUF_ALIGN_H, np.float16, (B, G.max_t, na, TENC))
+    np.testing.assert_array_equal(ah[:, NP:NP + GEN - 1].view(np.uint16), al.astype(np.float16).view(np.uint16))
+    ah = ah[:, NP:NP + GEN - 1].astype(np.float32)
     e.close()
     ctx.close()
 
@@ -127,6 +134,13 @@ def test_greedy_tokens_and_timestamps_turbo_widths():
         np.testing.assert_array_equal(ts_dev[b][:k], ts_ref[:k], err_msg=f"row {b} timestamps (blocks {blocks[b]})")
         ts_checked += k
         ts_equal_all += int(np.sum(ts_dev[b] == ts_ref))
+        # a caller that keeps src/transcribe.rs:147-162 as it is: the fp16 rows (download_h) into align.rs's
+        # arithmetic, against the oracle's probabilities rounded to fp16 as the reference's kernel rounds them
+        ts_h = transcribe.jump_times(ah[b], TENC, 7, True)
+        probs_h = probs[b].astype(np.float16).astype(np.float32)
+        ts_href = R.token_timestamps(probs_h[:, :, None], [(s, 0) for s in range(na)], NP, NP + GEN, 2 * TENC,
+                                     half=True)[NP:NP + GEN - 1]
+        np.testing.assert_array_equal(ts_h[:k], ts_href[:k], err_msg=f"row {b} timestamps from fp16 rows")
     print(f"turbo widths, 32 rows x {GEN} generated tokens (graph replay): tokens equal to the oracle's choices at "
           f"{tok_checked} positions, timestamps equal at {ts_checked} rows before each row's first margin <= "
           f"{MARGIN} ({ts_equal_all} of {B * (GEN - 1)} rows equal over the whole table); alignment rows max error "
