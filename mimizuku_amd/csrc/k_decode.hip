@@ -129,7 +129,12 @@ typedef __attribute__((address_space(3))) void lds_void;
 constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 
-constexpr int MZ_NT = 2;  // cache-policy bit of a buffer load: nontemporal (weights are streamed once per step)
+// Cache policy of the decoder's streams. The cross keys / values (983 MB per 32-row turbo step) and the LM head's
+// tied embedding (133 MB) are read nontemporally; the projection weights (183 MB) with the default policy, so they
+// stay in the memory-side cache from one step to the next while the nontemporal streams pass through: their
+// latency-bound launches then wait less for memory (32-row step 415.1 -> 399.7 us; with the LM head cached as well
+// the 316 MB exceed the 256 MB cache and the step took 418 us).
+constexpr int MZ_NT = 2;  // cache-policy bit of a buffer load: nontemporal
 
 // One workgroup per (32 output columns, K slice, 32 rows): both operands of its K slice (<= MZ_DEC_KSLICE) go from
 // memory straight into LDS with every load issued at once (buffer_load ... lds, 16 bytes per lane), in 1 KB blocks of
@@ -165,7 +170,7 @@ __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rX, LDSP(sx + i * 512), 16, (unsigned)(rg * 8 + r8) * ldx2 + col, 0, 0,
                                                  0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, LDSP(sw + i * 512), 16,
-                                                 (unsigned)(n0 + rg * 8 + r8) * (unsigned)p.K * 2u + col, 0, 0, MZ_NT);
+                                                 (unsigned)(n0 + rg * 8 + r8) * (unsigned)p.K * 2u + col, 0, 0, 0);
     }
     // epilogue operands
     float bv[NC];
