@@ -761,8 +761,12 @@ static int step_impl(mz_engine* e, int b, int lang, int prompt_len) {
         return hipMemcpyAsync(e->dtrace + (size_t)l * e->bmax * D, e->x, (size_t)b * D * 4, hipMemcpyDeviceToDevice, s);
     };
     if (dtr) TRY(dtrace(0), "decoder trace");
+    // the projection weights stay in the memory-side cache between steps when all layers' fit it with room to spare
+    // (large-v3-turbo: 183 MB of 256) and the batch has two rows or more; otherwise they stream nontemporally
+    const bool w_cached = (size_t)nl * (6 * (size_t)D * D + 2 * (size_t)D * F) * 2 <= ((size_t)200 << 20) && b >= 2;
     auto gemm = [&](int epi, const f16* x, int ldx, const Lin& L, int N, int K, int ks, void* out, long ldo) {
         MzDec g{};
+        g.w_nt = w_cached ? 0 : 1;
         g.x = x;
         g.ldx = ldx;
         g.W = L.w;

@@ -130,10 +130,12 @@ constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (
 
 
 // Cache policy of the decoder's streams. The cross keys / values (983 MB per 32-row turbo step) and the LM head's
-// tied embedding (133 MB) are read nontemporally; the projection weights (183 MB) with the default policy, so they
-// stay in the memory-side cache from one step to the next while the nontemporal streams pass through: their
-// latency-bound launches then wait less for memory (32-row step 415.1 -> 399.7 us; with the LM head cached as well
-// the 316 MB exceed the 256 MB cache and the step took 418 us).
+// tied embedding (133 MB) are read nontemporally. The projection weights are read with the default policy when the
+// caller sets w_nt = 0 (the engine does when all layers' projections fit the 256 MB memory-side cache with room to
+// spare, as large-v3-turbo's 183 MB do, and the batch has at least two rows): they then stay in that cache from one
+// step to the next while the nontemporal streams pass through, and the latency-bound projections wait less for
+// memory (32-row turbo step 415.1 -> 399.7 us). large-v3's 1.47 GB cannot stay, and there, as at one row, the
+// nontemporal loads are faster (3.07 -> 2.98 ms and 248 -> 245 us per step).
 constexpr int MZ_NT = 2;  // cache-policy bit of a buffer load: nontemporal
 
 // One workgroup per (32 output columns, K slice, 32 rows): both operands of its K slice (<= MZ_DEC_KSLICE) go from
@@ -169,8 +171,11 @@ __global__ void __launch_bounds__(256) dec_gemm_kernel(const MzDec p) {
         const unsigned col = (unsigned)(kb + g * 64 + c * 8) * 2;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rX, LDSP(sx + i * 512), 16, (unsigned)(rg * 8 + r8) * ldx2 + col, 0, 0,
                                                  0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, LDSP(sw + i * 512), 16,
-                                                 (unsigned)(n0 + rg * 8 + r8) * (unsigned)p.K * 2u + col, 0, 0, 0);
+        const unsigned ow = (unsigned)(n0 + rg * 8 + r8) * (unsigned)p.K * 2u + col;
+        if (p.w_nt)  // (the policy is an immediate of the instruction: one load per branch, a uniform branch)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, LDSP(sw + i * 512), 16, ow, 0, 0, MZ_NT);
+        else
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, LDSP(sw + i * 512), 16, ow, 0, 0, 0);
     }
     // epilogue operands
     float bv[NC];

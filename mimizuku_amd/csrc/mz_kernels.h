@@ -82,6 +82,7 @@ struct MzDec {
     const unsigned char* sup;
     int bs1, bs2, prompt_len;
     void* amax;  // int2 {float bits, id} [mz_lm_blocks(N)][M]
+    int w_nt;    // projections: W read nontemporally (1) or with the default policy (0); the LM head always streams
 };
 hipError_t mz_dec_gemm_launch(hipStream_t s, int epi, const MzDec& g);
 // LM head workgroups (each with one argmax partial per row) and vocabulary tiles of 16 per workgroup
