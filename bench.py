@@ -65,9 +65,9 @@ def dec_kernel_bytes(g, B: int, p: int, na: int) -> dict:
         "dec_self": B * 2 * (p + 1) * d * 2 + B * d * 4 + act,
         "dec_oproj": d * d * 2 + act + ks_dd * B * d * 4,
         "dec_addln": B * d * 4 * (ks_dd + 2) + act,
-        # keys and values, the query weights, the residual add of the out-projection's partials (read x and the
-        # partials, write the new residual) and the output, the alignment rows
-        "dec_cross": B * 2 * 1500 * d * 2 + d * d * 2 + B * d * 4 * (ks_dd + 2) + act + B * (na / nl) * 1500 * 4,
+        # keys and values, the query weights, the LayerNorm rows in and the output out, the alignment rows (fp32 and
+        # their fp16 copies)
+        "dec_cross": B * 2 * 1500 * d * 2 + d * d * 2 + 2 * act + B * (na / nl) * 1500 * (4 + 2),
         "dec_xo": d * d * 2 + act + ks_dd * B * d * 4,
         "dec_fc1": ff * d * 2 + act + B * ff * 2,
         "dec_fc2": d * ff * 2 + B * ff * 2 + ks_df * B * d * 4,
