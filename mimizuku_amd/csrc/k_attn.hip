@@ -10,9 +10,9 @@
 // fp16, are directly the B operand of O^T = V^T P^T, and V^T (written transposed by the QKV GEMM) is read with
 // 16-byte LDS loads.
 //
-// On this part the vector ALU and the matrix cores of a SIMD do not overlap (an MFMA and the vector instructions
-// around it take the sum of their times), so every vector instruction per score counts: the running max is set by
-// the first block and later blocks compute no max at all; a block is recomputed against its own max (and O
+// Vector work hides only in part under the matrix cores (a wave's own vector instructions overlap about two thirds
+// of their time with its independent products, the other wave of the SIMD covers more), so every vector instruction
+// per score counts: the running max is set by the first block and later blocks compute no max at all; a block is recomputed against its own max (and O
 // rescaled) only when the sum of its probabilities reaches 2^12, i.e. some p = exp2(s - m) could leave the range
 // where fp16 holds it exactly enough; the probabilities are rounded two per packed conversion and summed two per
 // dot2 instruction, and the key mask of the padded last tile is applied in that tile only.
