@@ -48,8 +48,15 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
     __shared__ __attribute__((aligned(16))) f16 sW1[BN * 64];
 
     const int nbn = (p.N + BN - 1) / BN, nbm = (p.M + BM - 1) / BM;
-    int bm, bn;
-    if (!xcd_tile(blockIdx.x, nbm, nbn, &bm, &bn)) return;
+    // Plain products run a persistent grid (one workgroup per CU) over xcd_tile's virtual tile order: workgroup w
+    // takes virtual tiles w, w + G, w + 2 G, ... (G a multiple of 8, so all of a workgroup's tiles lie on its XCD),
+    // and the next tile's first K tile is requested before this tile's epilogue runs, so its round trip and the
+    // workgroup's dispatch are not paid once per tile. The convolution takes one tile per workgroup.
+    constexpr bool PERSIST = ALOAD == ALOAD_PLAIN;
+    const int nvirt = 8 * ((nbm + 7) >> 3) * nbn, vstep = PERSIST ? (int)gridDim.x : nvirt;
+    int v = blockIdx.x, bm = 0, bn = 0;
+    while (v < nvirt && !xcd_tile(v, nbm, nbn, &bm, &bn)) v += vstep;
+    if (v >= nvirt) return;
     // the wave index through readfirstlane: wave-uniform values (tile origins, store descriptors) stay scalar
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 2, wn = wave & 3, lr = lane & 31, lh = lane >> 5;
@@ -57,7 +64,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
     // behind the K loop instead of stalling the products' end. One unconditional buffer load per column block (a
     // missing bias is a descriptor of no bytes, which reads zeros): a branch would make the compiler wait for the
     // load at once. Kept as fp16 until used.
-    const int n0 = bn * BN + wn * WN;
+    int n0 = bn * BN + wn * WN;
     const __amdgpu_buffer_rsrc_t rB = rsrc(p.bias, p.bias ? (unsigned)p.N * 2 : 0u);
     f16 bias_h[TN];
 #pragma unroll
@@ -71,16 +78,23 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
 
     const __amdgpu_buffer_rsrc_t rW = rsrc(p.W, (unsigned)p.N * p.K * 2);
     unsigned voW[WR];
+    auto set_w = [&](int bn_) {
 #pragma unroll
-    for (int r = 0; r < WR; r++) voW[r] = (unsigned)(bn * BN + wave * (BN / NW) + 8 * r + lrow) * p.K * 2 + (lc ^ (r & 1)) * 16;
+        for (int r = 0; r < WR; r++)
+            voW[r] = (unsigned)(bn_ * BN + wave * (BN / NW) + 8 * r + lrow) * p.K * 2 + (lc ^ (r & 1)) * 16;
+    };
+    set_w(bn);
     __amdgpu_buffer_rsrc_t rA;
     unsigned voA[AR];
     int srow[AR], stime[AR];  // conv: source row of tap 0 and its time index (-1 .. tin - 1), or a row past M
-    if (ALOAD == ALOAD_PLAIN) {
-        rA = rsrc(p.A, (unsigned)p.M * p.lda * 2);
+    auto set_a = [&](int bm_) {
 #pragma unroll
         for (int r = 0; r < AR; r++)
-            voA[r] = (unsigned)(bm * BM + wave * (BM / NW) + 8 * r + lrow) * p.lda * 2 + (lc ^ (r & 1)) * 16;
+            voA[r] = (unsigned)(bm_ * BM + wave * (BM / NW) + 8 * r + lrow) * p.lda * 2 + (lc ^ (r & 1)) * 16;
+    };
+    if (ALOAD == ALOAD_PLAIN) {
+        rA = rsrc(p.A, (unsigned)p.M * p.lda * 2);
+        set_a(bm);
     } else {
         const int clips = p.M / p.conv_tout;
         rA = rsrc(p.A, (unsigned)clips * p.conv_tin * p.conv_cin * 2);
@@ -179,30 +193,18 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    // two K tiles per iteration, one per LDS buffer (distinct arrays, so the compiler sees that the loads in flight
-    // never alias the tile being read); an odd last tile is left in buffer 0
-    issue(0, sA0, sW0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    frags(sA0, sW0, 0, fa0, fw0);
-    int kt = 0;
-    for (; kt + 1 < nk; kt += 2) {
-        tile(kt, sA0, sW0, sA1, sW1);
-        tile(kt + 1, sA1, sW1, sA0, sW0);
-    }
-    if (kt < nk) tile(kt, sA0, sW0, sA1, sW1);
-
     // epilogue: acc[i][j] element r is row m0 + i * 32 + 8 (r / 4) + 4 lh + r % 4, column n0 + j * 32 + lr
-    const int m0 = bm * BM + wm * WM;
+    auto epilogue = [&](const int m0, const int n0) {
     if (EPI == EPI_HEADS) {
-        if (p.kind == 3) __syncthreads();  // every wave is done reading operands: LDS is free for the v transposes
+        if (p.kind == 3) lds_barrier();  // every wave is done reading operands: LDS is free for the v transposes
         const int blk = n0 >> 6;           // a wave's columns lie in one 64-wide head block (WN <= 64)
         const bool vt = p.kind == 3 && blk / p.nh == 2;
         if (vt) {
             // encoder v: stage each 32-row slice of the wave's tile in LDS as [column][row] (the wave's own 32 x WN
-            // halves of sA0: 8 waves x 32 x WN <= BM x 64) and write runs of 4 token positions
-            static_assert(NW * 32 * WN <= BM * 64, "staging slice exceeds sA0");
-            f16* st = sA0 + wave * (32 * WN);
+            // halves of sW1, which the next tile's first loads leave alone: 8 waves x 32 x WN <= BN x 64) and write
+            // runs of 4 token positions
+            static_assert(NW * 32 * WN <= BN * 64, "staging slice exceeds sW1");
+            f16* st = sW1 + wave * (32 * WN);
 #pragma unroll
             for (int i = 0; i < TM; i++) {
 #pragma unroll
@@ -333,13 +335,75 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
                 ((float*)p.out)[(long)m * p.ldo + n] = gelu_erf(v) + (float)p.pos[(long)(m % MZ_TENC) * p.N + n];
             }
     }
+    };
+
+    // two K tiles per iteration, one per LDS buffer (distinct arrays, so the compiler sees that the loads in flight
+    // never alias the tile being read); an odd last tile is left in buffer 0. After the K loop every read of both
+    // buffers is done (the last tile's barrier), so the next tile's first K tile can go to buffer 0 at once.
+    issue(0, sA0, sW0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    frags(sA0, sW0, 0, fa0, fw0);
+    for (;;) {
+        int kt = 0;
+        for (; kt + 1 < nk; kt += 2) {
+            tile(kt, sA0, sW0, sA1, sW1);
+            tile(kt + 1, sA1, sW1, sA0, sW0);
+        }
+        if (kt < nk) tile(kt, sA0, sW0, sA1, sW1);
+        const int m0 = bm * BM + wm * WM, n0c = n0;
+        int vn = v + vstep, bmn = 0, bnn = 0;
+        while (vn < nvirt && !xcd_tile(vn, nbm, nbn, &bmn, &bnn)) vn += vstep;
+        const bool more = PERSIST && vn < nvirt;
+        f16 bias_n[TN];
+        if (more) {  // the next tile's biases and first K tile, in flight during this epilogue
+            // (the biases first: the compiler waits for their registers before the epilogue, and loads complete in
+            // order, so the K tile issued after them stays in flight)
+            n0 = bnn * BN + wn * WN;
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                bias_n[j] = __builtin_bit_cast(
+                    f16, __builtin_amdgcn_raw_buffer_load_b16(rB, (unsigned)(n0 + j * 32 + lr) * 2, 0, 0));
+            set_a(bmn);
+            set_w(bnn);
+            issue(0, sA0, sW0);
+        }
+        epilogue(m0, n0c);
+        if (!more) break;
+        v = vn;
+        bm = bmn;
+        bn = bnn;
+#pragma unroll
+        for (int j = 0; j < TN; j++) bias_h[j] = bias_n[j];
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j] = f32x16{};
+        __builtin_amdgcn_s_waitcnt(0);  // the next tile's first K tile has landed (and this tile's stores)
+        __syncthreads();
+        frags(sA0, sW0, 0, fa0, fw0);
+    }
 #endif
+}
+
+// compute units of the current device (workgroups of a persistent grid: one per CU), a multiple of 8
+int cu_groups() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 256;
+        cached[dev] = n / 8 * 8;
+    }
+    return cached[dev];
 }
 
 template <int BM, int BN, int ALOAD, int EPI>
 hipError_t launch(hipStream_t s, const MzGemm& g) {
     const int nbm = (g.M + BM - 1) / BM, nbn = (g.N + BN - 1) / BN;
-    const int grid = 8 * ((nbm + 7) / 8) * nbn;
+    const int nvirt = 8 * ((nbm + 7) / 8) * nbn;
+    const int cus = cu_groups(), grid = ALOAD == ALOAD_PLAIN && nvirt > cus ? cus : nvirt;
     hipLaunchKernelGGL((gemm_kernel<BM, BN, ALOAD, EPI>), dim3(grid), dim3(NW * 64), 0, s, g);
     return hipGetLastError();
 }
