@@ -95,6 +95,66 @@ __global__ void __launch_bounds__(512) dec_add_ln_kernel(const float* xin, float
     ln_row4(v, on, dim, wv, bv, y + (long)row * dim, eps, red);
 }
 
+// dec_add_ln_kernel's work with one wave per row for NC float4 per lane (dim = 256 NC) and NP partials: every load of
+// the row (residual, partials, bias, gamma, beta: 6 NC + 3 NC requests per lane) is issued before the first use, the
+// residual is summed in dec_add_ln_kernel's order (the same x), and the LayerNorm statistics are two-pass sums over
+// the wave through DPP and lane reads, so no barrier and no LDS are needed.
+template <int NC, int NP>
+__global__ void __launch_bounds__(64) dec_add_ln_wave_kernel(const float* xin, float* x, const float* __restrict__ parts,
+                                                              long part_stride, const f16* __restrict__ bias,
+                                                              const f16* __restrict__ w, const f16* __restrict__ b,
+                                                              f16* __restrict__ y, float eps) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    constexpr int dim = 256 * NC;
+    const int row = blockIdx.x, lane = threadIdx.x;
+    const long r0 = (long)row * dim;
+    f32x4 v[NC], pp[NP][NC];
+    f16x4 bb[NC], wv[NC], bv[NC];
+#pragma unroll
+    for (int i = 0; i < NC; i++) v[i] = *(const f32x4*)(xin + r0 + (lane + 64 * i) * 4);
+#pragma unroll
+    for (int s = 0; s < NP; s++)
+#pragma unroll
+        for (int i = 0; i < NC; i++) pp[s][i] = *(const f32x4*)(parts + s * part_stride + r0 + (lane + 64 * i) * 4);
+    const __amdgpu_buffer_rsrc_t rB = rsrc(bias, bias ? (unsigned)dim * 2u : 0u);
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+        const unsigned o = (unsigned)(lane + 64 * i) * 8u;
+        bb[i] = __builtin_bit_cast(f16x4, __builtin_amdgcn_raw_buffer_load_b64(rB, o, 0, 0));
+        wv[i] = *(const f16x4*)(w + (lane + 64 * i) * 4);
+        bv[i] = *(const f16x4*)(b + (lane + 64 * i) * 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every request above is issued before anything waits for data
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+#pragma unroll
+        for (int s = 0; s < NP; s++) v[i] += pp[s][i];
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[i][e] += (float)bb[i][e];
+        *(f32x4*)(x + r0 + (lane + 64 * i) * 4) = v[i];
+        sum += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
+    }
+    const float mean = wave_sum(sum) / dim;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < NC; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float d = v[i][e] - mean;
+            q = fmaf(d, d, q);
+        }
+    const float rstd = rsqrtf(wave_sum(q) / dim + eps);
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) o[e] = (v[i][e] - mean) * rstd * (float)wv[i][e] + (float)bv[i][e];
+        st4(y + r0 + (lane + 64 * i) * 4, o[0], o[1], o[2], o[3]);
+    }
+#endif
+}
+
 __global__ void __launch_bounds__(512) dec_embed_ln_kernel(const int* __restrict__ tok, int* __restrict__ ctr,
                                                            const f16* __restrict__ emb, const f16* __restrict__ pe,
                                                            float* __restrict__ x, const f16* __restrict__ w,
@@ -955,6 +1015,12 @@ hipError_t mz_dec_add_ln_launch(hipStream_t s, const float* xin, float* x, const
                                 long part_stride, const f16* bias, const f16* w, const f16* b, f16* y, int rows,
                                 int dim, float eps) {
     if (dim % 4 != 0 || dim > 2048 || rows <= 0 || nparts < 0 || nparts > MZ_MAX_PARTS) return hipErrorInvalidValue;
+    // one wave per row for the decoder width of large-v3 and large-v3-turbo with its five split-K partials
+    if (dim == 1280 && nparts == 5) {
+        hipLaunchKernelGGL((dec_add_ln_wave_kernel<5, 5>), dim3(rows), dim3(64), 0, s, xin, x, parts, part_stride, bias,
+                           w, b, y, eps);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(dec_add_ln_kernel, dim3(rows), dim3(row_threads(dim)), 0, s, xin, x, parts, nparts, part_stride,
                        bias, w, b, y, dim, eps);
     return hipGetLastError();
