@@ -95,6 +95,35 @@ __global__ void __launch_bounds__(512) dec_add_ln_kernel(const float* xin, float
     ln_row4(v, on, dim, wv, bv, y + (long)row * dim, eps, red);
 }
 
+// LayerNorm of one row held by one wave, NC float4 per lane (v[i] = x[4 (lane + 64 i) ..]), written to y as fp16:
+// two-pass statistics over the wave through DPP and lane reads (no LDS, no barrier)
+template <int NC>
+__device__ __forceinline__ void ln_wave(const f32x4 (&v)[NC], const f16x4 (&wv)[NC], const f16x4 (&bv)[NC],
+                                        f16* __restrict__ y, float eps) {
+    constexpr int dim = 256 * NC;
+    const int lane = threadIdx.x & 63;
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < NC; i++) sum += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
+    const float mean = wave_sum(sum) / dim;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < NC; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float d = v[i][e] - mean;
+            q = fmaf(d, d, q);
+        }
+    const float rstd = rsqrtf(wave_sum(q) / dim + eps);
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) o[e] = (v[i][e] - mean) * rstd * (float)wv[i][e] + (float)bv[i][e];
+        st4(y + (lane + 64 * i) * 4, o[0], o[1], o[2], o[3]);
+    }
+}
+
 // dec_add_ln_kernel's work with one wave per row for NC float4 per lane (dim = 256 NC) and NP partials: every load of
 // the row (residual, partials, bias, gamma, beta: 6 NC + 3 NC requests per lane) is issued before the first use, the
 // residual is summed in dec_add_ln_kernel's order (the same x), and the LayerNorm statistics are two-pass sums over
@@ -125,7 +154,6 @@ __global__ void __launch_bounds__(64) dec_add_ln_wave_kernel(const float* xin, f
         bv[i] = *(const f16x4*)(b + (lane + 64 * i) * 4);
     }
     __builtin_amdgcn_sched_barrier(0);  // every request above is issued before anything waits for data
-    float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < NC; i++) {
 #pragma unroll
@@ -133,25 +161,8 @@ __global__ void __launch_bounds__(64) dec_add_ln_wave_kernel(const float* xin, f
 #pragma unroll
         for (int e = 0; e < 4; e++) v[i][e] += (float)bb[i][e];
         *(f32x4*)(x + r0 + (lane + 64 * i) * 4) = v[i];
-        sum += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
     }
-    const float mean = wave_sum(sum) / dim;
-    float q = 0.f;
-#pragma unroll
-    for (int i = 0; i < NC; i++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float d = v[i][e] - mean;
-            q = fmaf(d, d, q);
-        }
-    const float rstd = rsqrtf(wave_sum(q) / dim + eps);
-#pragma unroll
-    for (int i = 0; i < NC; i++) {
-        float o[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) o[e] = (v[i][e] - mean) * rstd * (float)wv[i][e] + (float)bv[i][e];
-        st4(y + r0 + (lane + 64 * i) * 4, o[0], o[1], o[2], o[3]);
-    }
+    ln_wave<NC>(v, wv, bv, y + r0, eps);
 #endif
 }
 
@@ -877,22 +888,22 @@ __global__ void __launch_bounds__(256, 1) dec_cross_wide_kernel(const MzDecCross
 // Token p + 1 of row b from the LM head's per-workgroup partials (value, id) (kernels/whisper.cu:451-493 rules:
 // the prompt positions stay; a finished row, or one whose every id is masked, gets eos). Workgroup 0 advances the
 // position for the next step.
-__global__ void __launch_bounds__(256) dec_argmax_kernel(const int2* __restrict__ amax, int nblk, int* __restrict__ tok,
-                                                         int* __restrict__ done, int* __restrict__ ctr, int B, int maxT,
-                                                         int prompt_len, int eos) {
-    __shared__ float sv[4];
-    __shared__ int si[4];
+__global__ void __launch_bounds__(64) dec_argmax_kernel(const int2* __restrict__ amax, int nblk, int* __restrict__ tok,
+                                                        int* __restrict__ done, int* __restrict__ ctr, int B, int maxT,
+                                                        int prompt_len, int eos) {
+    // one wave per row: lane l takes partials l, l + 64, ... (all of one batch of 8 in flight together), then the
+    // wave's reduction; the lowest id wins ties, so the choice does not depend on the order
     const int b = blockIdx.x, tid = threadIdx.x;
     const int p = ctr[1];
     if (b == 0 && tid == 0) ctr[0] = p + 1;
     if (p + 1 < prompt_len || p + 1 >= maxT) return;
     float best = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i0 = tid; i0 < nblk; i0 += 256 * 8) {
+    for (int i0 = tid; i0 < nblk; i0 += 64 * 8) {
         int2 r[8];
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const int i = i0 + 256 * u;
+            const int i = i0 + 64 * u;
             r[u] = i < nblk ? amax[(long)i * B + b] : make_int2(__float_as_int(-INFINITY), 0x7fffffff);
         }
 #pragma unroll
@@ -905,17 +916,7 @@ __global__ void __launch_bounds__(256) dec_argmax_kernel(const int2* __restrict_
         }
     }
     wave_argmax(best, bi);
-    if ((tid & 63) == 0) {
-        sv[tid >> 6] = best;
-        si[tid >> 6] = bi;
-    }
-    __syncthreads();
     if (tid == 0) {
-        for (int w = 1; w < 4; w++)
-            if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
-                best = sv[w];
-                bi = si[w];
-            }
         const int t = (done[b] || bi == 0x7fffffff) ? eos : bi;
         tok[(long)b * maxT + p + 1] = t;
         if (t == eos) done[b] = 1;
@@ -1037,7 +1038,7 @@ hipError_t mz_dec_embed_ln_launch(hipStream_t s, const int* tok, int* ctr, const
 hipError_t mz_dec_argmax_launch(hipStream_t s, const int2* amax, int nblk, int* tok, int* done, int* ctr, int B,
                                 int maxT, int prompt_len, int eos) {
     if (B <= 0 || nblk <= 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(dec_argmax_kernel, dim3(B), dim3(256), 0, s, amax, nblk, tok, done, ctr, B, maxT, prompt_len,
+    hipLaunchKernelGGL(dec_argmax_kernel, dim3(B), dim3(64), 0, s, amax, nblk, tok, done, ctr, B, maxT, prompt_len,
                        eos);
     return hipGetLastError();
 }
