@@ -407,7 +407,7 @@ def main():
         return
     if a.gpus != 1:
         print("bench.py measures one GPU: this path shards over clips with no exchange step, and multi-GPU runs "
-              "are not part of this build (use --gpus 1)", file=sys.stderr)
+              "are not supported here (use --gpus 1)", file=sys.stderr)
         sys.exit(2)
 
     import ctypes as C

@@ -139,7 +139,7 @@ typedef struct {
 size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int eg);
 /* Validates the geometry (Dims::load checks, src/model.rs:47-59) and allocates the engine for bmax decoded rows and
  * eg clips per encoder pass (Engine::new, src/model.rs:333-514, minus reading files). Beyond the reference's limits
- * this build needs d % 128 == 0 and d <= 1280 (every Whisper size; larger widths are refused with MZ_ERR_ARG);
+ * the library needs d % 128 == 0 and d <= 1280 (every Whisper size; larger widths are refused with MZ_ERR_ARG);
  * bmax has no upper limit besides memory, as the reference's --batch. */
 int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, int bmax, int eg, mz_engine** out);
 #define MZ_DT_F16 0

@@ -177,9 +177,9 @@ int run(int argc, const char* const* argv) {
     };
     const char* model_dir = args.get("--model");
     if (!model_dir) throw Err{"--model is required (see --help)"};
-    if (args.get("--ref")) throw Err{"--ref: the reference-comparison mode is not part of this build"};
+    if (args.get("--ref")) throw Err{"--ref: the reference-comparison mode is not supported by this tool"};
     if (args.get("--enc-attn") && !strcmp(args.get("--enc-attn"), "cublas"))
-        throw Err{"--enc-attn cublas: this build has only the fused encoder attention"};
+        throw Err{"--enc-attn cublas: only the fused encoder attention is available"};
     const double t_start = now();
 
     std::vector<std::string> paths = args.files;

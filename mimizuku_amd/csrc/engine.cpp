@@ -266,7 +266,7 @@ extern "C" size_t mz_scratch_bytes(const mz_dims* d, int n_align, int bmax, int 
 extern "C" int mz_engine_new(mz_ctx* c, const mz_dims* d, const mz_gencfg* g, int bmax, int eg, mz_engine** out) {
     if (!c || !d || !g || !out) return mz_fail(MZ_ERR_ARG, "mz_engine_new: null argument");
     *out = nullptr;
-    // geometry limits (Dims::load, src/model.rs:47-59) plus this build's: d % 128 == 0 and d <= 1280 (the decoder's
+    // geometry limits (Dims::load, src/model.rs:47-59) plus the library's own: d % 128 == 0 and d <= 1280 (the decoder's
     // unsplit products, the LM head and the cross-attention's query projection hold a whole row of K in LDS)
     if (d->nh * HD != d->d || d->d % 128 || d->d > MZ_DEC_KSLICE || d->ff % 64 || d->ff <= 0 || d->n_mels % 8 ||
         d->n_mels <= 0 || d->max_t < 16 || d->max_t > 448 || d->max_t % 8 || d->enc_layers < 1 || d->enc_layers > 64 ||

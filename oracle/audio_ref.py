@@ -1,6 +1,6 @@
 """CPU oracle for the audio front end — TEST INFRASTRUCTURE ONLY.
 
-Only tests/ may import this module, and only as the checker. Nothing in the mimizuku_amd package imports it.
+Only tests/ may import this module, and only to check results. Nothing in the mimizuku_amd package imports it.
 
 A numpy restatement of the reference's features (src/audio.rs): WAV reading (read_wav, :14-75), resampling to
 16 kHz (to_16k, :77-145), the mel filters and windowed DFT basis (Mel::new, :146-193) and the log-mel features

@@ -1,6 +1,6 @@
 """CPU oracle for the text side — TEST INFRASTRUCTURE ONLY.
 
-Only tests/ may import this module, and only as the checker. Nothing in the mimizuku_amd package imports it.
+Only tests/ may import this module, and only to check results. Nothing in the mimizuku_amd package imports it.
 
 A Python restatement of the reference's tokenizer decoding (src/tok.rs: GPT-2's byte table, decode with the clean-up
 of spaces, whole-character pieces with times) and of the CLI's JSON result (src/main.rs:97-138). Pinned by the

@@ -1,6 +1,6 @@
 """Writes the tiny-geometry golden vectors from transformers' Whisper modules (fp32, CPU).
 
-Run in the build container only (transformers 5.15.0 installed; the GPU box never runs this):
+Run where transformers 5.15.0 is installed (the GPU tests only read the vectors it writes):
     PYTHONPATH=. python tests/golden/make_golden.py
 
 The model is built offline from a local WhisperConfig and loaded with the seeded weights of mimizuku_amd.synth (no

@@ -1,6 +1,6 @@
 """Writes log-mel golden vectors from transformers' WhisperFeatureExtractor (its numpy path and its torch path).
 
-Run in the build container only (transformers 5.15.0 installed; the GPU box never runs this):
+Run where transformers 5.15.0 is installed (the GPU tests only read the vectors it writes):
     PYTHONPATH=. python tests/golden/make_mel_golden.py
 
 The waveforms are synthetic and regenerated from `waves.waveform(seed, seconds)`: a chirp plus a tone plus noise,

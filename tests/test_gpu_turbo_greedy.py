@@ -1,7 +1,7 @@
 """Greedy tokens and token timestamps at the benchmark's widths against the oracle (large-v3-turbo decoder: d 1280,
 20 heads, 4 layers, vocabulary 51866, 6 alignment heads), 32 rows, 44 generated tokens by graph replay.
 
-The north-star rule: identical greedy token ids and 20 ms-grid timestamps wherever the oracle's top-2 logit margin
+The acceptance rule: identical greedy token ids and 20 ms-grid timestamps wherever the oracle's top-2 logit margin
 exceeds 1e-2. The engine decodes greedily (the captured step replayed, as the product does); the oracle is then
 teacher-forced on the engine's sequences, and for every row, up to its first position where the oracle's margin is
 at most 1e-2:

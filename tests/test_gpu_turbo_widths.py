@@ -16,7 +16,7 @@ alignment-head rows are compared with the oracle's, and the greedy choice after 
 top-2 margin exceeds 1e-2. Bars as in test_gpu_engine.py, except the alignment rows: max-abs error <= 2e-3 x the
 largest probability. These rows are nearly uniform (the largest ~0.01), and each probability carries the relative
 error of its score, ~1e-3 here from the fp16 rounding of the LayerNorm output that feeds the query (the oracle keeps
-it in fp32; the reference rounds it, as this build does).
+it in fp32; the reference rounds it, as the kernels here do).
 
 At the benchmark's own positions (200 .. 203, the self-attention cache holding 200+ keys) every decoder layer is
 checked layer-local on the engine's residual trace, and the logits of its final residual against the oracle's head;

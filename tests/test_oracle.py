@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/whisper_ref.py) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/whisper_ref.py) before results are checked against it.
 
 * against the golden vectors transformers 5.15.0 wrote for the tiny geometry (tests/golden/make_golden.py);
 * against the reference's own known-answer tests (src/align.rs:112-139);

@@ -177,7 +177,7 @@ def test_cli_arguments(tmp_path, capfd):
                        (["--model", str(tmp_path), "a.wav"], "config.json: cannot read"),
                        (["--model", str(tmp_path), "--dir", str(tmp_path / "nope")], "cannot read the directory"),
                        (["--model", str(tmp_path), "--enc-attn", "cublas", "a.wav"], "fused encoder attention"),
-                       (["--model", str(tmp_path), "--ref", "r.safetensors", "a.wav"], "not part of this build")]:
+                       (["--model", str(tmp_path), "--ref", "r.safetensors", "a.wav"], "not supported by this tool")]:
         assert cli(*args) == 1, args
         assert what in capfd.readouterr().err, args
     synth.write_model_dir(str(tmp_path), synth.TINY, {"x": np.zeros(1, np.float16)})
