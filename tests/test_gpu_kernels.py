@@ -303,6 +303,36 @@ def test_gemm_large_qkv_shape(ctx):
         ctx.free(p)
 
 
+@pytest.mark.parametrize("m,n,k", [(9000, 2304, 320), (12000, 768, 448), (6000, 1000, 192)])
+def test_gemm_persistent_shapes(ctx, m, n, k):
+    """Products with more tiles than CUs, so each workgroup of the persistent grid walks several tiles (requesting the
+    next tile's first K tile before each epilogue): 256 x 256 tiles with a partial last block row and an odd count
+    of 64-wide K tiles (9000 x 2304 x 320), 256 x 128 tiles (12000 x 768 x 448), 128 x 128 tiles with partial block
+    rows and columns (6000 x 1000 x 192); fp16 output against float64 on sampled rows, and on the first shape also
+    the GELU and fp32 residual epilogues."""
+    rng = np.random.default_rng(m + n + k)
+    x, w, b = f16(rng, (m, k)), f16(rng, (n, k), 0.05), f16(rng, (n,), 0.1)
+    dx, dw, db = (ctx.upload_new(a) for a in (x, w, b))
+    rows = np.r_[rng.choice(m, 300, replace=False), m - 40:m]
+    acc = x[rows].astype(np.float64) @ w.astype(np.float64).T + b
+    dy = ctx.alloc(m * n * 2)
+    L.check(L.lib().mz_gemm(ctx.h, dx, k, dw, dy, n, m, n, k, db))
+    assert_f16(ctx.download(dy, (m, n), np.float16)[rows], acc)
+    if m == 9000:
+        L.check(L.lib().mz_linear(ctx.h, linear_args(epilogue=L.EPI_GELU_F16, a=dx, lda=k, w=dw, bias=db, m=m, n=n,
+                                                     k=k, out=dy, ldo=n)))
+        assert_f16(ctx.download(dy, (m, n), np.float16)[rows], R.gelu(acc.astype(np.float32)))
+        res = rng.standard_normal((m, n)).astype(np.float32)
+        dr = ctx.upload_new(res)
+        L.check(L.lib().mz_linear(ctx.h, linear_args(epilogue=L.EPI_RESID_F32, a=dx, lda=k, w=dw, bias=db, m=m, n=n,
+                                                     k=k, out=dr, ldo=n)))
+        got = ctx.download(dr, (m, n), np.float32)
+        assert rel_err(got[rows], res[rows] + acc) < 1e-5
+        ctx.free(dr)
+    for p in (dx, dw, db, dy):
+        ctx.free(p)
+
+
 def test_conv_stem_implicit_gemm(ctx):
     """mel transpose + conv1 (k 3, pad 1) + GELU, conv2 (stride 2) + GELU + positions, against the oracle's conv1d."""
     rng = np.random.default_rng(6)
