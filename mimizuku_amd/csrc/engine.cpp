@@ -1038,8 +1038,8 @@ using clk = std::chrono::steady_clock;
 static double since(clk::time_point a) { return std::chrono::duration<double>(clk::now() - a).count(); }
 
 // Enqueues the encoder of a chunk of n clips and returns (the first half of transcribe, src/transcribe.rs:107-116):
-// its groups go round-robin over two lanes (the main stream and the engine's second stream, each with its own
-// scratch), and one event marks them all done. One chunk at a time: collect it before submitting the next.
+// its groups go round-robin over the encoder lanes (the main stream and the engine's other streams, each with its
+// own scratch), and one event marks them all done. One chunk at a time: collect it before submitting the next.
 static int submit_impl(mz_engine* e, const float* mels, bool on_device, int n) {
     if (!e || !mels) return mz_fail(MZ_ERR_ARG, "mz_transcribe_submit: null argument");
     if (!e->loaded) return mz_fail(MZ_ERR_STATE, "mz_transcribe_submit: weights not loaded (mz_engine_finish)");
@@ -1048,18 +1048,20 @@ static int submit_impl(mz_engine* e, const float* mels, bool on_device, int n) {
     const auto t0 = clk::now();
     const int nm = e->dm.n_mels, ngroups = (n + e->eg - 1) / e->eg;
     const int nlanes = e->trace_on ? 1 : std::min(ngroups, MZ_ENC_LANES);
-    hipStream_t st[2] = {e->c->stream, e->ls[0]};
+    hipStream_t st[MZ_ENC_LANES];  // lane 0: the engine's stream; lane k: its own stream ls[k - 1]
+    st[0] = e->c->stream;
+    for (int k = 1; k < MZ_ENC_LANES; k++) st[k] = e->ls[k - 1];
     if (nlanes > 1) {
         TRY(hipEventRecord(e->fork, st[0]), "hipEventRecord");
-        TRY(hipStreamWaitEvent(st[1], e->fork, 0), "hipStreamWaitEvent");
+        for (int k = 1; k < nlanes; k++) TRY(hipStreamWaitEvent(st[k], e->fork, 0), "hipStreamWaitEvent");
     }
     for (int g0 = 0, gi = 0; g0 < n; g0 += e->eg, gi++) {
         const int gn = std::min(e->eg, n - g0), k = gi % nlanes;
         if (int r = encode_impl(e, mels + (size_t)g0 * nm * NFR, on_device, gn, g0, k, st[k], e->xkvbuf)) return r;
     }
-    if (nlanes > 1) {
-        TRY(hipEventRecord(e->join[0], st[1]), "hipEventRecord");
-        TRY(hipStreamWaitEvent(st[0], e->join[0], 0), "hipStreamWaitEvent");
+    for (int k = 1; k < nlanes; k++) {
+        TRY(hipEventRecord(e->join[k - 1], st[k]), "hipEventRecord");
+        TRY(hipStreamWaitEvent(st[0], e->join[k - 1], 0), "hipStreamWaitEvent");
     }
     TRY(hipEventRecord(e->enc_done, st[0]), "hipEventRecord");
     e->pending_n = n;
