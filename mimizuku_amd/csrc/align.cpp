@@ -50,8 +50,6 @@ float mz_h2f_host(uint16_t h) {
 extern "C" uint16_t mz_f2h(float x) { return mz_f2h_host(x); }
 extern "C" float mz_h2f(uint16_t h) { return mz_h2f_host(h); }
 
-static inline float rh(float x) { return mz_h2f_host(mz_f2h_host(x)); }
-
 // DTW over cost m [rows][cols] with a float32 cost table; ties go to the horizontal move (j - 1). Cells are filled
 // row by row: each depends only on its left, upper and upper-left neighbours, so the table equals the column-order
 // fill of the numpy reference while walking memory contiguously.
