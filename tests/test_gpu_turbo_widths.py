@@ -239,10 +239,11 @@ def test_graph_replay_at_position_200_equals_eager():
 
 
 def test_cross_attention_variants_give_the_same_bits():
-    """The cross-attention runs as one of two variants chosen by the batch: at most 12 rows (one workgroup per CU, two
-    batches of keys staged in LDS) or more (three workgroups per CU, half a batch staged). Where the keys come from
-    does not change the arithmetic: the same 12 rows stepped in a batch of 32 and in a batch of 12 give the same bits
-    (tokens, logits, alignment rows, residual stream), greedy from a 4-token prompt through 6 positions."""
+    """The cross-attention runs as one of two forms chosen by the batch: more than 12 rows (three workgroups per CU,
+    half a batch of keys staged) or at most 12 (one workgroup per CU, two batches staged). Where the keys come from
+    does not change the arithmetic: the first rows stepped in a batch of 32 and alone in batches of 12, 3, 2 and 1
+    give the same bits (tokens, logits, alignment rows, residual stream), greedy from a 4-token prompt through 6
+    positions."""
     rng = np.random.default_rng(24)
     W = synth.random_weights(G, seed=9, bias_std=0.02, ln_std=0.1)
     gen = synth.generation_config(G, align_heads=[[2, 4], [2, 11], [3, 3], [3, 6], [3, 11], [3, 14]])
@@ -260,13 +261,15 @@ def test_cross_attention_variants_give_the_same_bits():
     ctx.upload(p, xkv)
     del xkv
     out = {}
-    for nb in (B, few):
+    for nb in (B, few, 3, 2, 1):
         e.reset(prompts[:nb])
         for _ in range(steps):
             e.step(nb, False, npr)
-        out[nb] = (e.tokens()[:few, :steps + 1], e.logits()[:few], e.align()[:few, :steps], e.dec_x()[:few])
-    for n, a, g in zip(("tokens", "logits", "alignment rows", "residual"), out[B], out[few]):
-        np.testing.assert_array_equal(a, g, err_msg=n)
-    print("cross-attention variants: 12 rows in a batch of 32 and alone give the same bits over", steps, "steps")
+        out[nb] = (e.tokens()[:nb, :steps + 1], e.logits()[:nb], e.align()[:nb, :steps], e.dec_x()[:nb])
+    for nb in (few, 3, 2, 1):
+        for n, a, g in zip(("tokens", "logits", "alignment rows", "residual"), out[B], out[nb]):
+            np.testing.assert_array_equal(a[:nb], g, err_msg=f"{n}, {nb} rows")
+    print("cross-attention forms: the first rows of a batch of 32 and alone in batches of 12, 3, 2 and 1 give the same "
+          "bits over", steps, "steps")
     e.close()
     ctx.close()
