@@ -10,16 +10,18 @@ constexpr int MAXC = 8;  // float4 chunks per lane: dim <= 2048
 
 // LayerNorm of one row held as v[i] = x[4 (lane + 64 i) .. + 4] (chunks past dim / 4 hold zeros and are not
 // stored), written to y as fp16. Two-pass statistics (mean, then the centred second moment) as the reference. The
-// gamma / beta loads go out before the reductions.
-__device__ __forceinline__ void ln_store(const float4 (&v)[MAXC], int nc, int lane, const f16* __restrict__ w,
-                                         const f16* __restrict__ b, f16* __restrict__ y, int dim, float eps) {
-    f16x4 wv[MAXC], bv[MAXC];
+// kernels request gamma and beta (ln_params) together with the row, so they cost no round trip of their own.
+__device__ __forceinline__ void ln_params(int nc, int lane, const f16* __restrict__ w, const f16* __restrict__ b,
+                                          f16x4 (&wv)[MAXC], f16x4 (&bv)[MAXC]) {
 #pragma unroll
     for (int i = 0; i < MAXC; i++)
         if (lane + 64 * i < nc) {
             wv[i] = *(const f16x4*)(w + (lane + 64 * i) * 4);
             bv[i] = *(const f16x4*)(b + (lane + 64 * i) * 4);
         }
+}
+__device__ __forceinline__ void ln_store_wb(const float4 (&v)[MAXC], int nc, int lane, const f16x4 (&wv)[MAXC],
+                                            const f16x4 (&bv)[MAXC], f16* __restrict__ y, int dim, float eps) {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < MAXC; i++)
@@ -54,9 +56,11 @@ __global__ void __launch_bounds__(256) ln_kernel(const float* __restrict__ x, lo
     const int nc = dim / 4;
     const float* xr = x + (long)row * ldx;
     float4 v[MAXC];
+    f16x4 wv[MAXC], bv[MAXC];
+    ln_params(nc, lane, w, b, wv, bv);
 #pragma unroll
     for (int i = 0; i < MAXC; i++) v[i] = lane + 64 * i < nc ? *(const float4*)(xr + (lane + 64 * i) * 4) : float4{};
-    ln_store(v, nc, lane, w, b, y + (long)row * ldy, dim, eps);
+    ln_store_wb(v, nc, lane, wv, bv, y + (long)row * ldy, dim, eps);
 }
 
 // x[r] += d[r] (fp16) in place, then y[r] = LN(x[r])
@@ -69,7 +73,8 @@ __global__ void __launch_bounds__(256) add_ln_kernel(float* __restrict__ x, cons
     float* xr = x + (long)row * dim;
     const f16* dr = d + (long)row * dim;
     float4 v[MAXC];
-    f16x4 dv[MAXC];
+    f16x4 dv[MAXC], wv[MAXC], bv[MAXC];
+    ln_params(nc, lane, w, b, wv, bv);  // gamma and beta in flight with the row, not a round trip after it
     // the residual and the delta are streamed once: nontemporal loads and stores
 #pragma unroll
     for (int i = 0; i < MAXC; i++) {
@@ -87,7 +92,7 @@ __global__ void __launch_bounds__(256) add_ln_kernel(float* __restrict__ x, cons
             v[i].w += (float)dv[i][3];
             __builtin_nontemporal_store(f32x4{v[i].x, v[i].y, v[i].z, v[i].w}, (f32x4*)(xr + (lane + 64 * i) * 4));
         }
-    ln_store(v, nc, lane, w, b, y + (long)row * dim, dim, eps);
+    ln_store_wb(v, nc, lane, wv, bv, y + (long)row * dim, dim, eps);
 }
 
 // mel f32 [G][nm][3000] -> f16 [G][3000][nm], 64 x 64 tiles through LDS
