@@ -1,7 +1,8 @@
 """CPU oracle for the Whisper compute path — TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the
-checker (or the timed CPU baseline). Nothing in the mimizuku_amd package imports it.
+reference that device results are compared against (or the timed CPU baseline). Nothing in the mimizuku_amd package
+imports it.
 
 An fp32 numpy restatement of transformers 5.15.0's Whisper modules (the oracle the reference verifies against,
 scripts/hf_reference.py:26-45), plus the reference's own greedy-choice rules (kernels/whisper.cu:451-493) and
