@@ -257,6 +257,20 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(const MzGemm p) {
         for (int i = 0; i < TM; i++) {
             const int mb = m0 + i * 32 + 4 * lh, gb = mb / MZ_TENC, tb = mb - gb * MZ_TENC;
             const unsigned cb = (unsigned)((gb - g0) * clip + (long)blk * (MZ_TPAD * MZ_HD)) + c0 + tb * MZ_HD;
+            if ((m0 + i * 32) / MZ_TENC == (m0 + i * 32 + 31) / MZ_TENC) {
+                // the block's 32 rows lie in one clip (wave-uniform; all but one block in 47 at 1500 rows per clip):
+                // each element's offset from cb is a constant, carried in the instruction's immediate offset
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int dr = 8 * (r >> 2) + (r & 3);
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        __builtin_amdgcn_raw_buffer_store_b16(
+                            __builtin_bit_cast(short, (f16)fmaf(acc[i][j][r], qsc, bv[j])), rH, cb * 2 + (dr * MZ_HD * 2 + j * 64),
+                            0, 0);
+                }
+                continue;
+            }
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int dr = 8 * (r >> 2) + (r & 3);
