@@ -5,7 +5,7 @@ accumulates in an order that does not depend on the clips beside it (the product
 whatever tile shape the batch size selects). So a clip's language, tokens and token timestamps are the same bits
 whether it is transcribed alone or in a batch: a property that holds at any batch size, checked here on six clips
 (two encoder groups on two lanes) against three of them alone (one group, smaller product tiles), in both timestamp
-modes, and for graph replay against eager steps. Turbo widths (d 1280, 20 heads, 4 decoder layers, 128 mels, the
+modes, for graph replay against eager steps, and for encoder groups of 2 and of 6 against groups of 4. Turbo widths (d 1280, 20 heads, 4 decoder layers, 128 mels, the
 51866-token vocabulary) with 2 encoder layers; random weights with non-zero biases and LayerNorm parameters.
 """
 import numpy as np
@@ -20,17 +20,27 @@ N, EG, MAX_NEW = 6, 4, 24
 
 
 @pytest.fixture(scope="module")
-def setup():
+def parts():
     W = synth.random_weights(G, seed=3, bias_std=0.02, ln_std=0.05)
     heads = synth.generation_config(synth.LARGE_V3_TURBO)["alignment_heads"]
     gen = synth.generation_config(G, align_heads=heads)
     dims = model.Dims(G.d, G.ff, G.nh, G.enc_layers, G.dec_layers, G.n_mels, G.vocab, G.max_t)
     gc = model.GenCfg.from_dict(gen, dims)
     ctx = model.Context(0)
-    e = model.Engine(ctx, dims, gc, N, EG)
-    e.load(W)
+
+    def engine(eg: int) -> model.Engine:
+        e = model.Engine(ctx, dims, gc, N, eg)
+        e.load(W)
+        return e
     mel = synth.synthetic_mel(N, G.n_mels, seed=5)
     prompt = transcribe.Prompt(gc, "auto", "transcribe")
+    yield engine, mel, prompt
+
+
+@pytest.fixture(scope="module")
+def setup(parts):
+    engine, mel, prompt = parts
+    e = engine(EG)
     yield e, mel, prompt
     e.close()
 
@@ -57,3 +67,19 @@ def test_graph_replay_equals_eager_steps(setup):
     eager, _ = transcribe.transcribe(e, mel, prompt, max_new=MAX_NEW, graph=False)
     for c in range(N):
         same(graph[c], eager[c], f"clip {c}")
+
+
+def test_encoder_group_size_does_not_change_results(setup, parts):
+    """The six clips encoded in groups of 2 (three groups over the two lanes) and in one group of 6 (one lane, larger
+    products) give the same bits as in groups of 4."""
+    e, mel, prompt = setup
+    engine = parts[0]
+    ref, _ = transcribe.transcribe(e, mel, prompt, max_new=MAX_NEW)
+    for eg in (2, N):
+        other = engine(eg)
+        try:
+            got, _ = transcribe.transcribe(other, mel, prompt, max_new=MAX_NEW)
+        finally:
+            other.close()
+        for c in range(N):
+            same(got[c], ref[c], f"clip {c}, groups of {eg}")
